@@ -1,0 +1,101 @@
+/*
+ * sparse_attn.h -- C-ABI of the MI355X (gfx950) sparse_attn hot path.
+ *
+ * The op: for every (batch b, query m, head h)
+ *
+ *   o[b,m,h,:] = sum_t softmax([s_0 .. s_{topk-1}, sink[h]])_t * kv[b, idx[b,m,t], :]
+ *   s_t        = scale * <q[b,m,h,:], kv[b, idx[b,m,t], :]>
+ *
+ * with the sink's own column dropped from the weighted sum. This is the
+ * reference oracle track-01/reference/reference.py:24-40 and the argument
+ * contract of track-01/requirements.md:92-114 (q, kv bf16; attn_sink fp32 per
+ * head; topk_idxs int32; o bf16 in q's layout).
+ *
+ * Index values:
+ *   -1                 padding sentinel: the slot is excluded (score -inf,
+ *                      its row is never read), as the sentinel handling of
+ *                      track-01/submission.py:313-322. A row whose slots are
+ *                      all -1 yields o = 0 (the sink takes all the mass).
+ *   0 .. kv_len-1      valid; duplicates count with multiplicity.
+ *   anything else      out of range: the slot is excluded, never read, and
+ *                      *err_word (if non-null) gets bit 0 set. The reference
+ *                      raises here (torch.gather at reference.py:28); the
+ *                      Python layer turns the flag into RuntimeError.
+ *
+ * Threading and ownership: the caller owns every buffer. The library keeps no
+ * mutable state apart from a per-device cache of the compute-unit count, and
+ * every entry point is reentrant. sa_forward is asynchronous on the given
+ * HIP stream.
+ */
+#ifndef SPARSE_ATTN_H
+#define SPARSE_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_ABI_VERSION 1
+
+/* Return codes. */
+enum {
+  SA_OK = 0,
+  SA_EINVAL = 1,        /* null pointer, negative size, bad stride or alignment */
+  SA_EUNSUPPORTED = 2,  /* h != 16, d != 512, or a grid beyond the launch limit */
+  SA_EWORKSPACE = 3,    /* workspace missing or smaller than sa_workspace_bytes */
+  SA_EHIP = 4           /* HIP runtime error (device query or launch) */
+};
+
+/*
+ * Arguments of one call. Strides are in elements. The innermost stride of q,
+ * kv and o (d) and of topk_idxs (topk) must be 1; q, kv and o must be 16-byte
+ * aligned with their other strides multiples of 8 elements.
+ */
+typedef struct sa_args {
+  const void* q;          /* bf16 [b, m, h, d]                            */
+  const void* kv;         /* bf16 [b, kv_len, d]  (K and V share rows)     */
+  const float* sink;      /* fp32 [h]                                      */
+  const int32_t* idx;     /* int32 [b, m, topk]                            */
+  void* o;                /* bf16 [b, m, h, d]  (written)                  */
+  int64_t b, m, h, d, kv_len, topk;
+  int64_t sq[4];          /* strides of q   */
+  int64_t skv[3];         /* strides of kv  */
+  int64_t sidx[3];        /* strides of idx */
+  int64_t so[4];          /* strides of o   */
+  float scale;            /* softmax scale, e.g. d**-0.5 */
+  void* workspace;        /* device scratch for split-topk partials */
+  size_t workspace_bytes;
+  int32_t* err_word;      /* device int32, nullable; bit 0 = bad index seen */
+} sa_args;
+
+/* Version of this ABI (SA_ABI_VERSION). */
+int sa_abi_version(void);
+
+/*
+ * Bytes of device workspace sa_forward needs for these arguments on the
+ * current HIP device (0 when no split-topk pass is planned). No counterpart
+ * in the reference: its Triton kernels keep all state on chip
+ * (track-01/submission.py:143-202); the output allocation it does replace
+ * is track-01/submission.py:1000.
+ */
+int sa_workspace_bytes(const sa_args* a, size_t* out_bytes);
+
+/*
+ * Run sparse attention on `hip_stream` (a hipStream_t; NULL = default
+ * stream). Replaces the body of sparse_attn in
+ * track-01/submission.py:975-1271 (argument unpacking :989-998, the launch
+ * of _sparse_attn_kernel_bf16 / _universal at :1005-1021 and :1225-1271).
+ * Argument errors return before any device work.
+ */
+int sa_forward(const sa_args* a, void* hip_stream);
+
+/* Static description of a return code. */
+const char* sa_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPARSE_ATTN_H */

@@ -1,0 +1,21 @@
+// sa_host_test.cpp -- g++-only build of the host-side argument validation and
+// split-topk planning (sa_plan.h), exported for CPU unit tests. Not part of the
+// product ABI; the HIP library compiles the same header.
+#include "sa_plan.h"
+
+extern "C" {
+
+int sa_host_validate(const sa_args* a) { return sa::validate(a); }
+
+int sa_host_plan(const sa_args* a, int num_cus, int64_t* nsplit, int64_t* split_len,
+                 size_t* ws_bytes) {
+  const int rc = sa::validate(a);
+  if (rc != SA_OK) return rc;
+  const sa::Plan p = sa::make_plan(a, num_cus);
+  *nsplit = p.nsplit;
+  *split_len = p.split_len;
+  *ws_bytes = p.ws_bytes;
+  return SA_OK;
+}
+
+}  // extern "C"

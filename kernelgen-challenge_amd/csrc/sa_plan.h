@@ -1,0 +1,100 @@
+// sa_plan.h -- host-side argument validation and launch planning for the
+// gfx950 sparse_attn kernels. Plain C++ (no HIP): the same code is compiled
+// into the HIP library and into a g++-built host test library.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sparse_attn.h"
+
+namespace sa {
+
+constexpr int kHeads = 16;        // h the kernels are built for
+constexpr int kDim = 512;         // d the kernels are built for
+constexpr int kTileRows = 64;     // gathered kv rows per pipeline step
+constexpr int64_t kMaxUnits = int64_t(1) << 24;  // work-groups per launch
+
+// Launch plan: the topk axis of every (b, m) query is cut into `nsplit`
+// contiguous parts of `split_len` slots; one work-group handles one part.
+struct Plan {
+  int64_t units;      // b * m
+  int nsplit;         // parts per query (1 = no combine pass)
+  int64_t split_len;  // slots per part
+  size_t ws_bytes;    // partial-state workspace (0 when nsplit == 1)
+};
+
+// Bytes of partial state per (query, part): running max and sum per head
+// (2 * 16 fp32) followed by the unnormalised output (16 * 512 fp32).
+constexpr size_t kPartialMLBytes = 2 * kHeads * sizeof(float);
+constexpr size_t kPartialOBytes = size_t(kHeads) * kDim * sizeof(float);
+
+inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+// Checks everything that does not need the device. Returns SA_OK or an error.
+inline int validate(const sa_args* a) {
+  if (a == nullptr) return SA_EINVAL;
+  if (a->b < 0 || a->m < 0 || a->h < 0 || a->d < 0 || a->kv_len < 0 ||
+      a->topk < 0)
+    return SA_EINVAL;
+  if (a->h != kHeads || a->d != kDim) return SA_EUNSUPPORTED;
+  if (a->b == 0 || a->m == 0) return SA_OK;  // empty output, nothing to read
+  if (a->q == nullptr || a->o == nullptr || a->sink == nullptr)
+    return SA_EINVAL;
+  if (a->topk > 0 && a->idx == nullptr) return SA_EINVAL;
+  if (a->kv_len > 0 && a->kv == nullptr) return SA_EINVAL;
+  if (a->kv_len > (int64_t(1) << 31) - 1) return SA_EUNSUPPORTED;
+  // unit inner strides
+  if (a->sq[3] != 1 || a->so[3] != 1 || a->skv[2] != 1) return SA_EINVAL;
+  if (a->topk > 0 && a->sidx[2] != 1) return SA_EINVAL;
+  // 16-byte row loads and stores
+  if (!aligned16(a->q) || !aligned16(a->o)) return SA_EINVAL;
+  if (a->kv_len > 0 && !aligned16(a->kv)) return SA_EINVAL;
+  for (int i = 0; i < 3; ++i)
+    if (a->sq[i] % 8 != 0 || a->so[i] % 8 != 0) return SA_EINVAL;
+  for (int i = 0; i < 2; ++i)
+    if (a->skv[i] % 8 != 0) return SA_EINVAL;
+  for (int i = 0; i < 3; ++i)
+    if (a->sq[i] < 0 || a->so[i] < 0) return SA_EINVAL;
+  if (a->skv[0] < 0 || a->skv[1] < 0) return SA_EINVAL;
+  if (a->sidx[0] < 0 || a->sidx[1] < 0) return SA_EINVAL;
+  if (!(a->scale == a->scale)) return SA_EINVAL;  // NaN scale
+  if (a->b > kMaxUnits || a->m > kMaxUnits || a->b * a->m > kMaxUnits)
+    return SA_EUNSUPPORTED;
+  return SA_OK;
+}
+
+// Split-topk plan. A query is cut only when there are fewer queries than
+// compute units, and never into parts shorter than one pipeline tile, so
+// decode shapes (few queries, long topk) still occupy every CU.
+inline Plan make_plan(const sa_args* a, int num_cus) {
+  Plan p{};
+  p.units = a->b * a->m;
+  p.nsplit = 1;
+  p.split_len = a->topk;
+  if (num_cus < 1) num_cus = 1;
+  if (p.units > 0 && p.units < num_cus && a->topk > kTileRows) {
+    int64_t want = (num_cus + p.units - 1) / p.units;
+    int64_t max_parts = (a->topk + kTileRows - 1) / kTileRows;
+    if (want > max_parts) want = max_parts;
+    if (want > 1) {
+      // parts are whole tiles so only the last one has a ragged tail
+      int64_t tiles = (a->topk + kTileRows - 1) / kTileRows;
+      int64_t tiles_per = (tiles + want - 1) / want;
+      p.split_len = tiles_per * kTileRows;
+      p.nsplit = int((a->topk + p.split_len - 1) / p.split_len);
+    }
+  }
+  if (p.units * p.nsplit > kMaxUnits) {  // keep the grid launchable
+    p.nsplit = 1;
+    p.split_len = a->topk;
+  }
+  p.ws_bytes = p.nsplit > 1
+                   ? size_t(p.units) * p.nsplit * (kPartialMLBytes + kPartialOBytes)
+                   : 0;
+  return p;
+}
+
+}  // namespace sa

@@ -1,0 +1,96 @@
+"""MI355X drop-in for track-01's ``sparse_attn``.
+
+Same module name and signature as the reference entry point
+(``track-01/submission.py:975``): put ``kernelgen-challenge_amd/`` on
+``sys.path`` and ``from submission import sparse_attn``.
+
+The call runs the hand-written gfx950 HIP kernels through the operator
+``torch.ops.sa_amd.sparse_attn_fwd`` (``csrc/sa_torch.cpp``), which calls the
+C-ABI ``sa_forward`` (``include/sparse_attn.h``) on torch's current stream.
+There is no other code path: if the extension is not built, or the tensors are
+not on a GPU, the call raises.
+
+Index handling (see ``include/sparse_attn.h``): ``-1`` slots are excluded;
+any other index outside ``[0, kv_len)`` raises ``RuntimeError`` as the
+reference oracle does (``torch.gather`` at ``reference.py:28``). That check
+reads a device flag back, which synchronises the stream; turn it off with
+``set_index_check(False)`` or ``SPARSE_ATTN_CHECK=0`` for asynchronous calls
+(bad indices are then skipped silently and never read).
+"""
+from __future__ import annotations
+
+import os
+import threading
+
+import torch
+
+__all__ = ["sparse_attn", "set_index_check", "index_check_enabled", "load_extension",
+           "extension_path"]
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+_EXT_PATH = os.path.join(_PKG_DIR, "lib", "sa_torch_ext.so")
+_lock = threading.Lock()
+_loaded = False
+_check = os.environ.get("SPARSE_ATTN_CHECK", "1") != "0"
+
+
+def extension_path() -> str:
+    return _EXT_PATH
+
+
+def load_extension() -> None:
+    """Load the in-tree operator library (idempotent). Raises if it is missing."""
+    global _loaded
+    if _loaded:
+        return
+    with _lock:
+        if _loaded:
+            return
+        if not os.path.exists(_EXT_PATH):
+            raise RuntimeError(
+                "sparse_attn: the gfx950 extension is not built "
+                f"({_EXT_PATH} missing); run `python kernelgen-challenge_amd/build.py`")
+        torch.ops.load_library(_EXT_PATH)
+        _loaded = True
+
+
+def set_index_check(enabled: bool) -> None:
+    """Turn the synchronous out-of-range index check on or off."""
+    global _check
+    _check = bool(enabled)
+
+
+def index_check_enabled() -> bool:
+    return _check
+
+
+def sparse_attn(q, kv, attn_sink, topk_idxs, scale):
+    """
+    Args:
+        q:          [b, m, h, d]   bf16   (h = 16, d = 512)
+        kv:         [b, kv_len, d] bf16   (K and V share rows)
+        attn_sink:  [h]            fp32
+        topk_idxs:  [b, m, topk]   int32  (-1 = padding slot)
+        scale:      float
+
+    Returns:
+        o:          [b, m, h, d]   bf16, a new tensor on q's device
+    """
+    if q.dim() != 4:
+        raise ValueError(f"q must be 4-D [b, m, h, d], got shape {tuple(q.shape)}")
+    if kv.dim() != 3 or attn_sink.dim() != 1 or topk_idxs.dim() != 3:
+        raise ValueError("expected kv [b, kv_len, d], attn_sink [h], topk_idxs [b, m, topk]")
+    if not (q.is_cuda and kv.is_cuda and attn_sink.is_cuda and topk_idxs.is_cuda):
+        raise ValueError("sparse_attn runs on the GPU only; move all inputs to the device")
+    load_extension()
+    # Same input handling as track-01/submission.py:995-998.
+    q_c = q.contiguous()
+    kv_c = kv.contiguous()
+    sink_c = attn_sink.contiguous()
+    idx_c = topk_idxs.contiguous()
+    err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
+    o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err)
+    if err is not None and int(err.item()) != 0:
+        raise RuntimeError(
+            f"sparse_attn: topk_idxs holds an index outside [-1, {kv.shape[1]})")
+    return o

@@ -1,0 +1,206 @@
+"""CPU tests of the C-ABI boundary (no GPU, no compute calls).
+
+* the HIP library loads and exports every function ``include/sparse_attn.h``
+  declares;
+* argument errors come back as return codes before any device work;
+* the g++ build of the host-side validation and split-topk planning
+  (``csrc/sa_plan.h``) behaves as documented;
+* the Python drop-in refuses CPU tensors (there is no CPU fallback).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(REPO, "kernelgen-challenge_amd")
+LIB = os.path.join(PKG, "lib")
+HEADER = os.path.join(REPO, "include", "sparse_attn.h")
+
+SA_OK, SA_EINVAL, SA_EUNSUPPORTED, SA_EWORKSPACE, SA_EHIP = range(5)
+
+
+class SaArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("kv", ctypes.c_void_p), ("sink", ctypes.c_void_p),
+        ("idx", ctypes.c_void_p), ("o", ctypes.c_void_p),
+        ("b", ctypes.c_int64), ("m", ctypes.c_int64), ("h", ctypes.c_int64),
+        ("d", ctypes.c_int64), ("kv_len", ctypes.c_int64), ("topk", ctypes.c_int64),
+        ("sq", ctypes.c_int64 * 4), ("skv", ctypes.c_int64 * 3),
+        ("sidx", ctypes.c_int64 * 3), ("so", ctypes.c_int64 * 4),
+        ("scale", ctypes.c_float), ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t), ("err_word", ctypes.c_void_p),
+    ]
+
+
+def _libs_built():
+    return all(os.path.exists(os.path.join(LIB, f)) for f in
+               ("libsparse_attn_gfx950.so", "sa_torch_ext.so", "libsa_host_test.so"))
+
+
+@pytest.fixture(scope="module")
+def libs():
+    if not _libs_built():  # build in-tree (hipcc cross-compiles without a GPU)
+        import importlib.util
+        spec = importlib.util.spec_from_file_location("sa_build", os.path.join(PKG, "build.py"))
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        mod.build()
+    hip = ctypes.CDLL(os.path.join(LIB, "libsparse_attn_gfx950.so"))
+    host = ctypes.CDLL(os.path.join(LIB, "libsa_host_test.so"))
+    for lib in (hip,):
+        lib.sa_forward.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_void_p]
+        lib.sa_workspace_bytes.argtypes = [ctypes.POINTER(SaArgs),
+                                           ctypes.POINTER(ctypes.c_size_t)]
+        lib.sa_strerror.restype = ctypes.c_char_p
+    host.sa_host_validate.argtypes = [ctypes.POINTER(SaArgs)]
+    host.sa_host_plan.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_int,
+                                  ctypes.POINTER(ctypes.c_int64),
+                                  ctypes.POINTER(ctypes.c_int64),
+                                  ctypes.POINTER(ctypes.c_size_t)]
+    return hip, host
+
+
+def good_args(b=1, m=4, kv_len=100, topk=64):
+    a = SaArgs()
+    a.q, a.kv, a.sink, a.idx, a.o = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    a.b, a.m, a.h, a.d, a.kv_len, a.topk = b, m, 16, 512, kv_len, topk
+    a.sq[:] = [m * 16 * 512, 16 * 512, 512, 1]
+    a.so[:] = [m * 16 * 512, 16 * 512, 512, 1]
+    a.skv[:] = [kv_len * 512, 512, 1]
+    a.sidx[:] = [m * topk, topk, 1]
+    a.scale = 512 ** -0.5
+    return a
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(sa_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_expected_api():
+    assert declared_functions() == ["sa_abi_version", "sa_forward", "sa_strerror",
+                                    "sa_workspace_bytes"]
+
+
+def test_library_exports_every_declared_symbol(libs):
+    hip, _ = libs
+    for name in declared_functions():
+        assert hasattr(hip, name), f"{name} not exported"
+    assert hip.sa_abi_version() == 1
+
+
+def test_strerror_covers_codes(libs):
+    hip, _ = libs
+    msgs = [hip.sa_strerror(c).decode() for c in range(5)]
+    assert msgs[0] == "ok" and len(set(msgs)) == 5
+    assert hip.sa_strerror(99).decode() == "unknown error"
+
+
+def test_forward_rejects_null_args(libs):
+    hip, host = libs
+    assert hip.sa_forward(None, None) == SA_EINVAL
+    assert host.sa_host_validate(None) == SA_EINVAL
+    ws = ctypes.c_size_t(0)
+    assert hip.sa_workspace_bytes(None, ctypes.byref(ws)) == SA_EINVAL
+    assert hip.sa_workspace_bytes(ctypes.byref(good_args()), None) == SA_EINVAL
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("h", 8, SA_EUNSUPPORTED), ("d", 256, SA_EUNSUPPORTED),
+    ("b", -1, SA_EINVAL), ("topk", -3, SA_EINVAL), ("kv_len", -1, SA_EINVAL),
+    ("q", 0, SA_EINVAL), ("o", 0, SA_EINVAL), ("sink", 0, SA_EINVAL),
+    ("idx", 0, SA_EINVAL), ("kv", 0, SA_EINVAL),
+    ("q", 0x10008, SA_EINVAL), ("o", 0x50002, SA_EINVAL), ("kv", 0x20004, SA_EINVAL),
+    ("scale", float("nan"), SA_EINVAL),
+])
+def test_forward_argument_errors(libs, field, value, code):
+    hip, host = libs
+    a = good_args()
+    setattr(a, field, value)
+    assert host.sa_host_validate(ctypes.byref(a)) == code
+    assert hip.sa_forward(ctypes.byref(a), None) == code
+
+
+@pytest.mark.parametrize("arr,i,value", [
+    ("sq", 3, 2), ("so", 3, 2), ("skv", 2, 2), ("sidx", 2, 2),
+    ("sq", 2, 500), ("so", 1, 12), ("skv", 1, 516), ("sq", 0, -8),
+])
+def test_forward_stride_errors(libs, arr, i, value):
+    hip, host = libs
+    a = good_args()
+    getattr(a, arr)[i] = value
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_EINVAL
+    assert hip.sa_forward(ctypes.byref(a), None) == SA_EINVAL
+
+
+def test_empty_shapes_are_ok_without_device_work(libs):
+    hip, host = libs
+    for b, m in ((0, 4), (3, 0)):
+        a = good_args(b=b, m=m)
+        a.q = a.o = a.kv = a.idx = a.sink = 0
+        assert host.sa_host_validate(ctypes.byref(a)) == SA_OK
+        assert hip.sa_forward(ctypes.byref(a), None) == SA_OK
+
+
+def test_optional_pointers(libs):
+    _, host = libs
+    a = good_args(topk=0)
+    a.idx = 0
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_OK  # no slots, no idx needed
+    a = good_args(kv_len=0)
+    a.kv = 0
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_OK  # only -1 slots possible
+
+
+def plan(host, a, cus):
+    ns, sl, ws = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_size_t()
+    rc = host.sa_host_plan(ctypes.byref(a), cus, ctypes.byref(ns), ctypes.byref(sl),
+                           ctypes.byref(ws))
+    assert rc == SA_OK
+    return ns.value, sl.value, ws.value
+
+
+PART_BYTES = 2 * 16 * 4 + 16 * 512 * 4
+
+
+@pytest.mark.parametrize("b,m,topk,cus,expect_ns,expect_len", [
+    (32, 1, 2048, 256, 8, 256),      # decode: 32 queries -> 8 parts of 4 tiles
+    (1, 4096, 2048, 256, 1, 2048),   # causal prefill: enough queries
+    (1, 64, 256, 256, 4, 64),        # plumbing: 4 parts of one tile
+    (1, 1024, 2048, 256, 1, 2048),   # long context
+    (64, 1, 128, 256, 2, 64),        # contest decode, topk 128
+    (1, 1, 640, 256, 10, 64),        # one query: one tile per part
+    (1, 1, 60, 256, 1, 60),          # shorter than a tile: never split
+    (1, 1, 4000, 80, 63, 64),
+])
+def test_split_plan(libs, b, m, topk, cus, expect_ns, expect_len):
+    _, host = libs
+    a = good_args(b=b, m=m, topk=topk, kv_len=5000)
+    ns, sl, ws = plan(host, a, cus)
+    assert (ns, sl) == (expect_ns, expect_len)
+    assert (ns - 1) * sl < topk <= ns * sl           # parts cover topk exactly
+    assert ws == (0 if ns == 1 else b * m * ns * PART_BYTES)
+
+
+def test_python_dropin_refuses_cpu_tensors():
+    import torch
+    import submission
+    q = torch.zeros(1, 2, 16, 512, dtype=torch.bfloat16)
+    kv = torch.zeros(1, 8, 512, dtype=torch.bfloat16)
+    sink = torch.zeros(16)
+    idx = torch.zeros(1, 2, 4, dtype=torch.int32)
+    with pytest.raises(ValueError):
+        submission.sparse_attn(q, kv, sink, idx, 0.1)
+    with pytest.raises(ValueError):
+        submission.sparse_attn(q[0], kv, sink, idx, 0.1)
+
+
+def test_torch_operator_registers(libs):
+    import torch
+    import submission
+    submission.load_extension()
+    assert hasattr(torch.ops.sa_amd, "sparse_attn_fwd")
+    schema = str(torch.ops.sa_amd.sparse_attn_fwd.default._schema)
+    assert "Tensor q" in schema and "float scale" in schema
