@@ -48,6 +48,15 @@ enum {
   SA_EHIP = 4           /* HIP runtime error (device query or launch) */
 };
 
+/* sa_args.flags bits (0 = let the library choose). */
+enum {
+  /* every query gathers its own rows (no shared-row tiles) */
+  SA_FLAG_PER_QUERY = 1u,
+  /* run every eligible tile of consecutive queries through the shared-row
+     kernel, whatever the overlap of their indices */
+  SA_FLAG_FORCE_TILES = 2u
+};
+
 /*
  * Arguments of one call. Strides are in elements. The innermost stride of q,
  * kv and o (d) and of topk_idxs (topk) must be 1; q, kv and o must be 16-byte
@@ -65,9 +74,10 @@ typedef struct sa_args {
   int64_t sidx[3];        /* strides of idx */
   int64_t so[4];          /* strides of o   */
   float scale;            /* softmax scale, e.g. d**-0.5 */
-  void* workspace;        /* device scratch for split-topk partials */
+  void* workspace;        /* device scratch: tile row unions, split partials */
   size_t workspace_bytes;
   int32_t* err_word;      /* device int32, nullable; bit 0 = bad index seen */
+  uint32_t flags;         /* SA_FLAG_* bits, normally 0 */
 } sa_args;
 
 /* Version of this ABI (SA_ABI_VERSION). */
@@ -75,7 +85,8 @@ int sa_abi_version(void);
 
 /*
  * Bytes of device workspace sa_forward needs for these arguments on the
- * current HIP device (0 when no split-topk pass is planned). No counterpart
+ * current HIP device: the row unions of shared-row tiles and the partial
+ * states of split-topk parts (0 when neither is planned). No counterpart
  * in the reference: its Triton kernels keep all state on chip
  * (track-01/submission.py:143-202); the output allocation it does replace
  * is track-01/submission.py:1000.

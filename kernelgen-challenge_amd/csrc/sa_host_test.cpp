@@ -18,4 +18,19 @@ int sa_host_plan(const sa_args* a, int num_cus, int64_t* nsplit, int64_t* split_
   return SA_OK;
 }
 
+// out[0..6] = nsplit, split_len, tiles, tiles_per_b, ntiles, tile_cap, ws_bytes
+int sa_host_plan_full(const sa_args* a, int num_cus, int64_t* out) {
+  const int rc = sa::validate(a);
+  if (rc != SA_OK) return rc;
+  const sa::Plan p = sa::make_plan(a, num_cus);
+  out[0] = p.nsplit;
+  out[1] = p.split_len;
+  out[2] = p.tiles ? 1 : 0;
+  out[3] = p.tiles_per_b;
+  out[4] = p.ntiles;
+  out[5] = p.tile_cap;
+  out[6] = int64_t(p.ws_bytes);
+  return SA_OK;
+}
+
 }  // extern "C"

@@ -15,13 +15,34 @@ constexpr int kDim = 512;         // d the kernels are built for
 constexpr int kTileRows = 64;     // gathered kv rows per pipeline step
 constexpr int64_t kMaxUnits = int64_t(1) << 24;  // work-groups per launch
 
-// Launch plan: the topk axis of every (b, m) query is cut into `nsplit`
-// contiguous parts of `split_len` slots; one work-group handles one part.
+// Shared-row tiles: kTileQueries consecutive queries of one batch gather the
+// union of their rows once. The union is built from a per-row count table in
+// LDS, so it needs kv_len <= kMaxTileKv.
+constexpr int kTileQueries = 4;
+constexpr int64_t kMaxTileKv = 32768;
+
+// Tile modes written by the index kernel.
+constexpr int kModePerQuery = 0;
+constexpr int kModeShared = 1;
+constexpr int kMetaInts = 4;  // per tile: union size, mode, valid slots, spare
+
+// Launch plan.
+//  * per-query kernel: the topk axis of every (b, m) query is cut into
+//    `nsplit` contiguous parts of `split_len` slots, one work-group per part,
+//    merged by the combine kernel when nsplit > 1;
+//  * shared-row path (`tiles`): an index kernel builds each tile's row union,
+//    then tiles whose queries overlap enough run in the shared-row kernel and
+//    the rest in the per-query kernel.
 struct Plan {
-  int64_t units;      // b * m
-  int nsplit;         // parts per query (1 = no combine pass)
-  int64_t split_len;  // slots per part
-  size_t ws_bytes;    // partial-state workspace (0 when nsplit == 1)
+  int64_t units;       // b * m
+  int nsplit;          // parts per query (1 = no combine pass)
+  int64_t split_len;   // slots per part
+  bool tiles;          // shared-row path enabled
+  int64_t tiles_per_b; // ceil(m / kTileQueries)
+  int64_t ntiles;      // b * tiles_per_b
+  int64_t tile_cap;    // union entries stored per tile (multiple of kTileRows)
+  size_t meta_off, rows_off, cnts_off, part_off;  // workspace byte offsets
+  size_t ws_bytes;     // total workspace
 };
 
 // Bytes of partial state per (query, part): running max and sum per head
@@ -33,6 +54,8 @@ inline bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
 
+inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
 // Checks everything that does not need the device. Returns SA_OK or an error.
 inline int validate(const sa_args* a) {
   if (a == nullptr) return SA_EINVAL;
@@ -40,12 +63,15 @@ inline int validate(const sa_args* a) {
       a->topk < 0)
     return SA_EINVAL;
   if (a->h != kHeads || a->d != kDim) return SA_EUNSUPPORTED;
+  if ((a->flags & ~uint32_t(SA_FLAG_PER_QUERY | SA_FLAG_FORCE_TILES)) != 0)
+    return SA_EINVAL;
   if (a->b == 0 || a->m == 0) return SA_OK;  // empty output, nothing to read
   if (a->q == nullptr || a->o == nullptr || a->sink == nullptr)
     return SA_EINVAL;
   if (a->topk > 0 && a->idx == nullptr) return SA_EINVAL;
   if (a->kv_len > 0 && a->kv == nullptr) return SA_EINVAL;
   if (a->kv_len > (int64_t(1) << 31) - 1) return SA_EUNSUPPORTED;
+  if (a->topk > (int64_t(1) << 31) - 1) return SA_EUNSUPPORTED;
   // unit inner strides
   if (a->sq[3] != 1 || a->so[3] != 1 || a->skv[2] != 1) return SA_EINVAL;
   if (a->topk > 0 && a->sidx[2] != 1) return SA_EINVAL;
@@ -68,7 +94,9 @@ inline int validate(const sa_args* a) {
 
 // Split-topk plan. A query is cut only when there are fewer queries than
 // compute units, and never into parts shorter than one pipeline tile, so
-// decode shapes (few queries, long topk) still occupy every CU.
+// decode shapes (few queries, long topk) still occupy every CU. Shared-row
+// tiles are planned when every query has its own work-group (no split), the
+// batch has at least one full tile and the count table fits in LDS.
 inline Plan make_plan(const sa_args* a, int num_cus) {
   Plan p{};
   p.units = a->b * a->m;
@@ -91,9 +119,27 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     p.nsplit = 1;
     p.split_len = a->topk;
   }
-  p.ws_bytes = p.nsplit > 1
-                   ? size_t(p.units) * p.nsplit * (kPartialMLBytes + kPartialOBytes)
-                   : 0;
+  p.tiles = p.nsplit == 1 && (a->flags & SA_FLAG_PER_QUERY) == 0 &&
+            a->m >= kTileQueries && a->topk > 0 && a->kv_len > 0 &&
+            a->kv_len <= kMaxTileKv;
+  size_t off = 0;
+  if (p.tiles) {
+    p.tiles_per_b = (a->m + kTileQueries - 1) / kTileQueries;
+    p.ntiles = a->b * p.tiles_per_b;
+    int64_t cap = a->kv_len < kTileQueries * a->topk ? a->kv_len : kTileQueries * a->topk;
+    p.tile_cap = int64_t(round_up(size_t(cap), kTileRows));
+    p.meta_off = off;
+    off = round_up(off + size_t(p.ntiles) * kMetaInts * 4, 256);
+    p.rows_off = off;
+    off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
+    p.cnts_off = off;
+    off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
+  }
+  if (p.nsplit > 1) {
+    p.part_off = off;
+    off += size_t(p.units) * p.nsplit * (kPartialMLBytes + kPartialOBytes);
+  }
+  p.ws_bytes = off;
   return p;
 }
 

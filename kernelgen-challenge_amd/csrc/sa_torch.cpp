@@ -16,7 +16,7 @@ namespace {
 at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
                            const at::Tensor& attn_sink,
                            const at::Tensor& topk_idxs, double scale,
-                           const c10::optional<at::Tensor>& err) {
+                           const c10::optional<at::Tensor>& err, int64_t flags) {
   TORCH_CHECK_VALUE(q.dim() == 4, "q must be [b, m, h, d], got ", q.sizes());
   TORCH_CHECK_VALUE(kv.dim() == 3, "kv must be [b, kv_len, d], got ", kv.sizes());
   TORCH_CHECK_VALUE(attn_sink.dim() == 1, "attn_sink must be [h], got ",
@@ -59,6 +59,8 @@ at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
   for (int i = 0; i < 3; ++i) a.sidx[i] = topk_idxs.stride(i);
   for (int i = 0; i < 4; ++i) a.so[i] = o.stride(i);
   a.scale = static_cast<float>(scale);
+  TORCH_CHECK_VALUE(flags >= 0 && flags <= 0xFFFFFFFFll, "bad flags ", flags);
+  a.flags = static_cast<uint32_t>(flags);
   if (err.has_value()) {
     TORCH_CHECK(err->device() == q.device() && err->scalar_type() == at::kInt &&
                     err->numel() >= 1 && err->is_contiguous(),
@@ -89,7 +91,7 @@ at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
 TORCH_LIBRARY(sa_amd, m) {
   m.def(
       "sparse_attn_fwd(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
-      "float scale, Tensor? err=None) -> Tensor");
+      "float scale, Tensor? err=None, int flags=0) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) { m.impl("sparse_attn_fwd", &sparse_attn_fwd); }

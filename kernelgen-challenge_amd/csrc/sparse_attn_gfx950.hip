@@ -4,30 +4,39 @@
 // Math (track-01/reference/reference.py:24-40): for each query (b, m) and
 // head h, s_t = scale * q[h] . kv[idx_t]; o[h] = sum_t softmax([s, sink[h]])_t
 // * kv[idx_t] with the sink column dropped; o cast to bf16 (round to nearest
-// even). -1 slots are excluded (track-01/submission.py:313-322).
+// even). -1 slots are excluded (track-01/submission.py:313-322); duplicated
+// indices count with multiplicity (gather semantics, reference.py:28).
 //
-// Kernel sa_fwd (one work-group of 4 wave64s per (query, topk part)):
-//   1. compact the part's valid slot indices into LDS (order kept; bad
-//      indices raise the error word and are dropped);
-//   2. loop over tiles of 64 gathered rows, double-buffered in LDS: every row
-//      is one coalesced 1 KiB wave load (64 lanes x 16 B) issued a full step
-//      ahead into registers and written to the idle buffer at the end of the
-//      step, so each row is read from memory once and shared by all 16 heads;
-//   3. S^T = K . Q^T with v_mfma_f32_16x16x32_bf16: wave w owns tile rows
-//      16w..16w+15 (M = rows, N = 16 heads, K = d = 512), Q^T held in
-//      registers for the whole call;
-//   4. online softmax in the log2 domain (scale * log2 e folded into the
-//      scores, exp2): per-head tile max across the 4 waves through LDS, P
-//      rounded to bf16 into LDS;
-//   5. O += P . V with the same MFMA: wave w owns d columns 128w..128w+127
-//      (M = 16 heads, N = d, K = 32 rows); V operands come from the same LDS
-//      rows through ds_read_b64_tr_b16 transposing reads, so K and V share one
-//      row-major copy;
-//   6. epilogue: fold the sink (m_tot = max(m, sink), as the max over scores
-//      and the sink in the reference's softmax) and store bf16, or store the
-//      part's (max, sum, unnormalised O) for the combine kernel.
-// Kernel sa_combine: merges the parts of one query with exp2(m_s - M)
-// weights, folds the sink and stores bf16.
+// Scores live in the log2 domain (scale * log2 e folded in, exp2) and the sink
+// is folded last as m_tot = max(m, sink), l_tot = 2^(m - m_tot) l +
+// 2^(sink - m_tot), which equals the reference's softmax over [s, sink]
+// (track-01/notes.md:32-41).
+//
+// Kernels
+// -------
+// sa_fwd_query_kernel  one work-group (4 wave64s) per (query, topk part):
+//   compacts the part's valid indices into LDS, then loops over tiles of 64
+//   gathered rows double-buffered in LDS (each row one coalesced 1 KiB wave
+//   load, prefetched a step ahead into registers). S^T = K . Q^T with
+//   v_mfma_f32_16x16x32_bf16 (wave w: tile rows 16w.., 16 heads, K = d = 512,
+//   Q^T resident in registers); online softmax with a per-head max across
+//   the waves through LDS; O += P . V with the same MFMA (wave w: d columns
+//   128w..), its V operands read from the same LDS rows by
+//   ds_read_b64_tr_b16 transposing reads. Writes bf16 o, or per-part
+//   (max, sum, unnormalised O) for sa_combine_kernel.
+// sa_tile_index_kernel  one work-group per tile of 4 consecutive queries:
+//   counts every valid index of the tile's queries in an LDS table (one byte
+//   per query), compacts the row union in ascending order with the packed
+//   counts, and marks the tile "shared" when the union is small enough that
+//   computing every (query, union row) pair wastes at most half the MFMA
+//   work; otherwise "per query".
+// sa_fwd_tile_kernel  one work-group per shared tile: gathers each union row
+//   once (LDS-DMA, 1 KiB per wave instruction) and computes all 64
+//   (query, head) columns against it: S^T = K . Q^T and O += P . V with
+//   v_mfma_f32_32x32x16_bf16; a row's multiplicity c enters as + log2(c) on
+//   its score (c = 0 masks it).
+// sa_combine_kernel  merges the topk parts of one (query, head), folds the
+//   sink and stores bf16.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -39,6 +48,8 @@ namespace {
 
 using sa::kDim;
 using sa::kHeads;
+using sa::kMetaInts;
+using sa::kModeShared;
 using sa::kTileRows;
 
 constexpr int kWaves = 4;
@@ -51,14 +62,26 @@ constexpr int kRowsPerWave = kTileRows / kWaves;  // 16
 constexpr int kDPerWave = kDim / kWaves;          // 128 output columns
 constexpr int kDBlocks = kDPerWave / 16;          // 8 MFMA column blocks
 constexpr float kLog2e = 1.4426950408889634f;
+// Lazy rescaling: the running reference max of a softmax column moves only
+// when a tile's max exceeds it by more than this (log2 units), so exp2(s - m)
+// stays below 2^8 and the accumulators are rescaled rarely.
+constexpr float kRescaleLog2 = 8.f;
+
+constexpr int kTQ = sa::kTileQueries;       // queries per shared tile
+constexpr int kCols = kTQ * kHeads;         // 64 (query, head) columns
+constexpr int kPPitch = kTileRows + 8;      // bf16 per P row in LDS (144 B)
 
 static_assert(kListCap % kThreads == 0, "compaction split");
 static_assert(kRowsPerWave == 16, "one 16-row MFMA block per wave");
+static_assert(kCols == 64 && kTileRows == 64, "shared tile wave layout");
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4_t;
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
 struct FwdParams {
   const __bf16* q;
@@ -68,6 +91,8 @@ struct FwdParams {
   __bf16* o;
   float* part;          // [units * nsplit] x (ml[32] + O[16*512]) when split
   int32_t* err;
+  const int32_t* tile_meta;  // non-null: skip queries of shared tiles
+  int64_t tiles_per_b;
   int64_t m, kv_len, topk;
   int64_t sq_b, sq_m, sq_h;
   int64_t skv_b, skv_n;
@@ -77,6 +102,34 @@ struct FwdParams {
   int nsplit;
   int64_t split_len;
   int64_t nblocks;      // grid size (units * nsplit)
+};
+
+struct IndexParams {
+  const int32_t* idx;
+  int32_t* err;
+  int32_t* meta;        // [ntiles][kMetaInts]
+  int32_t* rows;        // [ntiles][cap]
+  uint32_t* cnts;       // [ntiles][cap], byte q = multiplicity in query q
+  int64_t m, kv_len, topk;
+  int64_t si_b, si_m;
+  int64_t tiles_per_b, cap;
+  int force;            // shared mode whenever the counts fit
+};
+
+struct TileParams {
+  const __bf16* q;
+  const __bf16* kv;
+  const float* sink;
+  __bf16* o;
+  const int32_t* meta;
+  const int32_t* rows;
+  const uint32_t* cnts;
+  int64_t m, cap, tiles_per_b;
+  int64_t sq_b, sq_m, sq_h;
+  int64_t skv_b, skv_n;
+  int64_t so_b, so_m, so_h;
+  float scale_log2;
+  int64_t nblocks;
 };
 
 struct CombineParams {
@@ -95,12 +148,44 @@ __device__ __forceinline__ f32x4 mfma_16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+__device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the address
 // of 4 consecutive bf16 (row j/4, columns 4*(j%4)..+3 of a 4 x 16 block) and
 // receives column j of that block (4 values, one per row).
 __device__ __forceinline__ bf16x4 lds_read_tr16(const uint8_t* p) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-      (lds_bf16x4_t*)((__attribute__((address_space(3))) uint8_t*)(p)));
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)((lds_u8_t*)(p)));
+}
+
+// LDS-DMA: every lane moves 16 (or 4) bytes from its own global address to
+// lds + lane * 16 (or 4); `lds` must be wave-uniform.
+__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)((lds_u8_t*)(lds)), 16, 0, 0);
+}
+
+__device__ __forceinline__ void lds_dma4(const void* gsrc, void* lds) {
+  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)((lds_u8_t*)(lds)), 4, 0, 0);
+}
+
+// Work-group barrier that orders LDS traffic only: waits for this wave's LDS
+// reads and writes (lgkmcnt = 0) but not for outstanding global loads, so a
+// prefetch issued earlier keeps flying across it. (__syncthreads() would also
+// drain every global load in flight.)
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt = max, expcnt = max, lgkmcnt = 0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Barrier after which this wave's LDS-DMA transfers are complete as well.
+__device__ __forceinline__ void dma_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 __device__ __forceinline__ float wave_max16(float x) {  // over lanes n, n+16, n+32, n+48
@@ -115,16 +200,10 @@ __device__ __forceinline__ float wave_sum16(float x) {
   return x;
 }
 
-// Logical unit for a work-group. Work-groups are dispatched round-robin over
-// the 8 XCDs; this maps each XCD's work-groups to a contiguous run of units
-// so neighbouring queries (which often share rows) share one L2.
-__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t nblocks) {
-  const int64_t per = nblocks / 8;
-  if (bid >= per * 8) return bid;
-  return (bid % 8) * per + bid / 8;
-}
-
-__global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) {
+// ============================================================================
+// per-query kernel
+// ============================================================================
+__global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kRowStride];
   __shared__ __attribute__((aligned(16))) int32_t s_list[kListCap];
   __shared__ __attribute__((aligned(16))) __bf16 s_p[kHeads * kTileRows];
@@ -137,11 +216,14 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
   const int n = lane & 15;   // MFMA column lane: head (S^T, P) or d (O)
   const int g = lane >> 4;   // MFMA k-group
 
-  const int64_t unit = xcd_remap(blockIdx.x, p.nblocks);
+  const int64_t unit = blockIdx.x;
   const int64_t qid = unit / p.nsplit;
   const int split = int(unit % p.nsplit);
   const int64_t bi = qid / p.m;
   const int64_t mi = qid % p.m;
+  if (p.tile_meta != nullptr &&
+      p.tile_meta[(bi * p.tiles_per_b + mi / kTQ) * kMetaInts + 1] == kModeShared)
+    return;  // this query belongs to a shared-row tile
   const int64_t s_begin = int64_t(split) * p.split_len;
   const int64_t s_end = min(p.topk, s_begin + p.split_len);
 
@@ -167,7 +249,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
   for (int64_t base = s_begin; base < s_end; base += kListCap) {
     const int cnt = int(min(int64_t(kListCap), s_end - base));
     __syncthreads();  // the previous batch is done with s_list
-    // ---- 1. compaction of this batch's valid slots --------------------------
+    // ---- compaction of this batch's valid slots -----------------------------
     int vals[kSlotsPerThread];
     int c = 0;
     bool bad = false;
@@ -205,7 +287,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
     if (nvalid == 0) continue;
     const int nsteps = (nvalid + kTileRows - 1) / kTileRows;
 
-    // ---- 2. gather pipeline ---------------------------------------------------
+    // ---- gather pipeline -----------------------------------------------------
     // wave w fetches tile rows 16w..16w+15; lane l moves bytes 16l..16l+15.
     bf16x8 pref[kRowsPerWave];
     auto fetch = [&](int step) {
@@ -231,7 +313,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
       const bool more = step + 1 < nsteps;
       if (more) fetch(step + 1);
 
-      // ---- 3. S^T = K . Q^T for rows 16w + (0..15) ---------------------------
+      // ---- S^T = K . Q^T for rows 16w + (0..15) ------------------------------
       f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
       {
         const uint8_t* krow = tb + (wave * kRowsPerWave + n) * kRowStride + 16 * g;
@@ -243,7 +325,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
       }
       // lane (n, g) now holds S[head n][tile row 16w + 4g + j], j = 0..3
 
-      // ---- 4. online softmax ---------------------------------------------------
+      // ---- online softmax ------------------------------------------------------
       const int rbase = step * kTileRows + wave * kRowsPerWave + 4 * g;
       float sv[4];
       float mx = -INFINITY;
@@ -254,31 +336,36 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
       }
       mx = wave_max16(mx);
       if (g == 0) s_red[wave][n] = mx;
-      __syncthreads();
+      lds_barrier();
+      // finite: every tile holds at least one valid row
       const float mstep = fmaxf(fmaxf(s_red[0][n], s_red[1][n]), fmaxf(s_red[2][n], s_red[3][n]));
-      const float m_new = fmaxf(m_run, mstep);  // finite: the tile has a valid row
-      const float alpha = exp2f(m_run - m_new);
+      float alpha = 1.f;
+      if (mstep > m_run + kRescaleLog2) {
+        alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mstep);  // O, l still 0 at first
+        m_run = mstep;
+      }
       float psum = 0.f;
       bf16x4 pb;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float pj = exp2f(sv[j] - m_new);
+        const float pj = exp2f(sv[j] - m_run);
         psum += pj;
         pb[j] = static_cast<__bf16>(pj);
       }
       l_run = l_run * alpha + psum;
-      m_run = m_new;
       *reinterpret_cast<bf16x4*>(&s_p[n * kTileRows + wave * kRowsPerWave + 4 * g]) = pb;
-      float aj[4];
+      if (__any(alpha != 1.f)) {
+        float aj[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) aj[j] = __shfl(alpha, 4 * g + j);
+        for (int j = 0; j < 4; ++j) aj[j] = __shfl(alpha, 4 * g + j);
 #pragma unroll
-      for (int blk = 0; blk < kDBlocks; ++blk)
+        for (int blk = 0; blk < kDBlocks; ++blk)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) oacc[blk][j] *= aj[j];
-      __syncthreads();
+          for (int j = 0; j < 4; ++j) oacc[blk][j] *= aj[j];
+      }
+      lds_barrier();
 
-      // ---- 5. O[:, 128w .. 128w+127] += P . V ---------------------------------
+      // ---- O[:, 128w .. 128w+127] += P . V -------------------------------------
 #pragma unroll
       for (int kk = 0; kk < kTileRows / 32; ++kk) {
         const bf16x8 pf =
@@ -294,11 +381,11 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
         }
       }
       if (more) stash((step + 1) & 1);
-      __syncthreads();
+      lds_barrier();
     }
   }
 
-  // ---- 6. epilogue ----------------------------------------------------------
+  // ---- epilogue ---------------------------------------------------------------
   float lw = wave_sum16(l_run);
   __syncthreads();
   if (g == 0) s_red[wave][n] = lw;
@@ -337,22 +424,370 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_kernel(const FwdParams p) 
   }
 }
 
-// One work-group per query: thread t owns head t/16, columns 32*(t%16)..+31.
-__global__ void __launch_bounds__(256) sa_combine_kernel(const CombineParams p) {
-  const int64_t qid = blockIdx.x;
+// ============================================================================
+// tile index kernel
+// ============================================================================
+__global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexParams p) {
+  extern __shared__ uint32_t s_count[];  // [kv_len], byte q = count in query q
+  __shared__ int s_wtot[kWaves];
+  __shared__ int s_nv[kTQ];
+  __shared__ int s_bsum[kTQ];
+  __shared__ int s_first;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t tile = blockIdx.x;
+  const int64_t bi = tile / p.tiles_per_b;
+  const int64_t q0 = (tile % p.tiles_per_b) * kTQ;
+  const int qt = int(min(int64_t(kTQ), p.m - q0));
+  const int kvl = int(p.kv_len);
+
+  for (int i = tid; i < kvl; i += kThreads) s_count[i] = 0u;
+  if (tid < kTQ) {
+    s_nv[tid] = 0;
+    s_bsum[tid] = 0;
+  }
+  if (tid == 0) s_first = kvl;
+  __syncthreads();
+
+  bool bad = false;
+  for (int qq = 0; qq < qt; ++qq) {
+    const int32_t* irow = p.idx + bi * p.si_b + (q0 + qq) * p.si_m;
+    int nv = 0;
+    for (int64_t t = tid; t < p.topk; t += kThreads) {
+      const int v = irow[t];
+      if (v >= 0 && v < kvl) {
+        atomicAdd(&s_count[v], 1u << (8 * qq));
+        ++nv;
+      } else if (v != -1) {
+        bad = true;
+      }
+    }
+    for (int off = 32; off > 0; off >>= 1) nv += __shfl_xor(nv, off);
+    if (lane == 0) atomicAdd(&s_nv[qq], nv);
+  }
+  if (bad && p.err != nullptr) atomicOr(p.err, 1);
+  __syncthreads();
+
+  // contiguous chunk per thread keeps the union in ascending row order
+  const int chunk = (kvl + kThreads - 1) / kThreads;
+  const int lo = min(kvl, tid * chunk);
+  const int hi = min(kvl, lo + chunk);
+  int c = 0;
+  int bsum[kTQ] = {0, 0, 0, 0};
+  int first = kvl;
+  for (int i = lo; i < hi; ++i) {
+    const uint32_t w = s_count[i];
+    if (w != 0u) {
+      if (c == 0) first = i;
+      ++c;
+#pragma unroll
+      for (int k = 0; k < kTQ; ++k) bsum[k] += int((w >> (8 * k)) & 255u);
+    }
+  }
+  int incl = c;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  if (lane == 63) s_wtot[wave] = incl;
+#pragma unroll
+  for (int k = 0; k < kTQ; ++k) {
+    int v = bsum[k];
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    if (lane == 0) atomicAdd(&s_bsum[k], v);
+  }
+  if (c > 0) atomicMin(&s_first, first);
+  __syncthreads();
+  int pos = incl - c;
+  int nU = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = s_wtot[w];
+    pos += (w < wave) ? t : 0;
+    nU += t;
+  }
+  int32_t* rows = p.rows + tile * p.cap;
+  uint32_t* cnts = p.cnts + tile * p.cap;
+  for (int i = lo; i < hi; ++i) {
+    const uint32_t w = s_count[i];
+    if (w != 0u) {
+      rows[pos] = i;
+      cnts[pos] = w;
+      ++pos;
+    }
+  }
+  // pad to whole 64-row steps with a valid row of count 0
+  const int padded = (nU + kTileRows - 1) / kTileRows * kTileRows;
+  for (int i = nU + tid; i < padded; i += kThreads) {
+    rows[i] = s_first;
+    cnts[i] = 0u;
+  }
+  if (tid == 0) {
+    bool overflow = false;
+    int total = 0;
+    for (int k = 0; k < kTQ; ++k) {
+      overflow |= s_bsum[k] != s_nv[k];  // a count passed 255 and carried
+      total += s_nv[k];
+    }
+    const bool shared =
+        !overflow && (p.force != 0 || int64_t(qt) * nU <= 2 * int64_t(total));
+    int32_t* meta = p.meta + tile * kMetaInts;
+    meta[0] = nU;
+    meta[1] = shared ? kModeShared : sa::kModePerQuery;
+    meta[2] = total;
+    meta[3] = overflow ? 1 : 0;
+  }
+}
+
+// ============================================================================
+// shared-row tile kernel
+// ============================================================================
+// Waves: w = 2c + r. For S^T, wave (r, c) owns union rows 32r..32r+31 of the
+// step and the 32 columns of queries 2c, 2c+1 (Q^T of those two queries is
+// resident: 32 k-steps of 16 d). For O, wave w owns d = 128w .. 128w+127 for
+// all 64 columns (2 x 4 blocks of 32 x 32 fp32 accumulators).
+__global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kRowStride];
+  __shared__ __attribute__((aligned(16))) __bf16 s_p[kCols * kPPitch];
+  __shared__ __attribute__((aligned(16))) uint32_t s_cnt[2][kTileRows];
+  __shared__ __attribute__((aligned(16))) float s_red[2][kCols];
+  __shared__ __attribute__((aligned(16))) float s_alpha[kCols];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = wave & 1;
+  const int c = wave >> 1;
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+
+  const int64_t tile = blockIdx.x;
+  const int32_t* meta = p.meta + tile * kMetaInts;
+  if (meta[1] != kModeShared) return;
+  const int nU = meta[0];
+  const int64_t bi = tile / p.tiles_per_b;
+  const int64_t q0 = (tile % p.tiles_per_b) * kTQ;
+  const int qt = int(min(int64_t(kTQ), p.m - q0));
+
+  // this lane's S^T column: query qq of the tile, head hh
+  const int col = 32 * c + l32;
+  const int qq = 2 * c + (l32 >> 4);
+  const int hh = l32 & 15;
+  bf16x8 qf[kDim / 16];
+  if (qq < qt) {
+    const __bf16* qrow = p.q + bi * p.sq_b + (q0 + qq) * p.sq_m + int64_t(hh) * p.sq_h + 8 * hi;
+#pragma unroll
+    for (int s = 0; s < kDim / 16; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
+  } else {
+#pragma unroll
+    for (int s = 0; s < kDim / 16; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = static_cast<__bf16>(0.f);
+  }
+
+  const int32_t* urows = p.rows + tile * p.cap;
+  const uint32_t* ucnts = p.cnts + tile * p.cap;
+  const __bf16* kvb = p.kv + bi * p.skv_b;
+  const int nsteps = (nU + kTileRows - 1) / kTileRows;
+
+  // Union rows of a step: lane i (< 16) of wave w holds row 16w + i; the
+  // gather reads them back with readlane so its addresses are scalar.
+  auto step_rows = [&](int step) -> int {
+    return urows[step * kTileRows + wave * kRowsPerWave + (lane & 15)];
+  };
+  auto fetch = [&](int rows_v, int step, int buf) {
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave; ++i) {
+      const int row = __builtin_amdgcn_readlane(rows_v, i);
+      lds_dma16(kvb + int64_t(row) * p.skv_n + 8 * lane,
+                &s_tile[buf][(wave * kRowsPerWave + i) * kRowStride]);
+    }
+    if (wave == 0) lds_dma4(ucnts + step * kTileRows + lane, &s_cnt[buf][0]);
+  };
+
+  float m_run = -INFINITY;  // running max of column `col` (log2 domain)
+  float l_run = 0.f;        // this lane's share of the column's sum
+  f32x16 oacc[2][4];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[mb][nb][i] = 0.f;
+
+  int rows_next = 0;
+  if (nsteps > 0) fetch(step_rows(0), 0, 0);
+  if (nsteps > 1) rows_next = step_rows(1);
+  dma_barrier();
+
+  for (int step = 0; step < nsteps; ++step) {
+    const int buf = step & 1;
+    if (step + 1 < nsteps) {
+      fetch(rows_next, step + 1, buf ^ 1);
+      if (step + 2 < nsteps) rows_next = step_rows(step + 2);
+    }
+    const uint8_t* tb = s_tile[buf];
+
+    // ---- S^T[rows 32r.., cols 32c..] = K . Q^T ---------------------------------
+    f32x16 sacc;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sacc[i] = 0.f;
+    {
+      // K fragments are read 4 k-steps ahead of the MFMA that uses them
+      const uint8_t* krow = tb + (32 * r + l32) * kRowStride + 16 * hi;
+      bf16x8 kf[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 32 * s);
+#pragma unroll
+      for (int s = 0; s < kDim / 16; ++s) {
+        const bf16x8 cur = kf[s & 3];
+        if (s + 4 < kDim / 16) kf[s & 3] = *reinterpret_cast<const bf16x8*>(krow + 32 * (s + 4));
+        sacc = mfma_32x32x16(cur, qf[s], sacc);
+      }
+    }
+    // lane holds column `col`, rows 32r + 8a + 4hi + b for register 4a + b
+
+    // ---- multiplicity, masking and the column max -------------------------------
+    // count c of each row in this lane's query: p = c * 2^(s - m), c = 0 masks
+    const int qshift = 8 * qq;
+    float sv[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const uint4 w4 = *reinterpret_cast<const uint4*>(&s_cnt[buf][32 * r + 8 * a + 4 * hi]);
+      const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const bool valid = ((ws[b] >> qshift) & 255u) != 0u;
+        sv[4 * a + b] = valid ? sacc[4 * a + b] * p.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sv[4 * a + b]);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    if (hi == 0) s_red[r][col] = mx;
+    lds_barrier();
+    const float mstep = fmaxf(s_red[0][col], s_red[1][col]);  // -inf: no row of this step
+    float alpha = 1.f;
+    if (mstep > m_run + kRescaleLog2) {
+      alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mstep);  // O, l still 0 at first
+      m_run = mstep;
+    }
+    const float mref = m_run == -INFINITY ? 0.f : m_run;  // column still empty
+    float psum = 0.f;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const uint4 w4 = *reinterpret_cast<const uint4*>(&s_cnt[buf][32 * r + 8 * a + 4 * hi]);
+      const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
+      bf16x4 pb;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float cnt = float((ws[b] >> qshift) & 255u);
+        const float pj = cnt * exp2f(sv[4 * a + b] - mref);
+        psum += pj;
+        pb[b] = static_cast<__bf16>(pj);
+      }
+      *reinterpret_cast<bf16x4*>(&s_p[col * kPPitch + 32 * r + 8 * a + 4 * hi]) = pb;
+    }
+    l_run = l_run * alpha + psum;
+    if (r == 0 && hi == 0) s_alpha[col] = alpha;
+    lds_barrier();
+
+    // ---- O[:, 128w..] = alpha * O + P . V --------------------------------------
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      float al[16];
+      bool any = false;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        const float4 a4 = *reinterpret_cast<const float4*>(&s_alpha[32 * mb + 8 * a + 4 * hi]);
+        al[4 * a + 0] = a4.x;
+        al[4 * a + 1] = a4.y;
+        al[4 * a + 2] = a4.z;
+        al[4 * a + 3] = a4.w;
+        any |= (a4.x != 1.f) | (a4.y != 1.f) | (a4.z != 1.f) | (a4.w != 1.f);
+      }
+      if (__any(any)) {
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[mb][nb][i] *= al[i];
+      }
+    }
+    const int G = lane >> 4;
+    const int j = lane & 15;
+#pragma unroll
+    for (int kb = 0; kb < kTileRows / 16; ++kb) {
+      bf16x8 pa[2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+        pa[mb] = *reinterpret_cast<const bf16x8*>(&s_p[(32 * mb + l32) * kPPitch + 16 * kb + 8 * hi]);
+      const uint8_t* vb = tb + (16 * kb + 8 * (G >> 1) + (j >> 2)) * kRowStride +
+                          (wave * kDPerWave + 16 * (G & 1) + 4 * (j & 3)) * 2;
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) {
+        const bf16x4 v0 = lds_read_tr16(vb + nb * 64);
+        const bf16x4 v1 = lds_read_tr16(vb + 4 * kRowStride + nb * 64);
+        const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) oacc[mb][nb] = mfma_32x32x16(pa[mb], vf, oacc[mb][nb]);
+      }
+    }
+    dma_barrier();  // every wave's prefetch has landed
+  }
+
+  // ---- epilogue: column sums, sink fold, bf16 store -----------------------------
+  const float lw = l_run + __shfl_xor(l_run, 32);
+  if (hi == 0) s_red[r][col] = lw;
+  __syncthreads();
+  if (r == 0 && hi == 0) {
+    const float lt = s_red[0][col] + s_red[1][col];
+    const float sink2 = p.sink[hh] * kLog2e;
+    const float mt = fmaxf(m_run, sink2);
+    const float a = exp2f(m_run - mt);  // 0 when the column has no valid slot
+    s_alpha[col] = a / (a * lt + exp2f(sink2 - mt));
+  }
+  __syncthreads();
+  __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + wave * kDPerWave + l32;
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float4 f4 = *reinterpret_cast<const float4*>(&s_alpha[32 * mb + 8 * a + 4 * hi]);
+      const float fs[4] = {f4.x, f4.y, f4.z, f4.w};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int qh = 32 * mb + 8 * a + 4 * hi + b;
+        const int q2 = qh >> 4;
+        if (q2 < qt) {
+          __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t(qh & 15) * p.so_h;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb)
+            orow[32 * nb] = static_cast<__bf16>(oacc[mb][nb][4 * a + b] * fs[b]);
+        }
+      }
+    }
+}
+
+// ============================================================================
+// split-topk combine: one 64-thread work-group per (query, head)
+// ============================================================================
+__global__ void __launch_bounds__(64) sa_combine_kernel(const CombineParams p) {
+  const int64_t qid = blockIdx.x / kHeads;
+  const int h = int(blockIdx.x % kHeads);
   const int64_t bi = qid / p.m;
   const int64_t mi = qid % p.m;
-  const int t = threadIdx.x;
-  const int h = t >> 4;
-  const int d0 = (t & 15) * 32;
+  const int d0 = threadIdx.x * 8;
   const float* part = p.part + qid * p.nsplit * kPartFloats;
 
   float M = -INFINITY;
   for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, part[s * kPartFloats + h]);
   float L = 0.f;
-  float acc[32];
+  float acc[8];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  for (int i = 0; i < 8; ++i) acc[i] = 0.f;
   for (int s = 0; s < p.nsplit; ++s) {
     const float* ps = part + s * kPartFloats;
     const float ms = ps[h];
@@ -360,27 +795,25 @@ __global__ void __launch_bounds__(256) sa_combine_kernel(const CombineParams p) 
     const float w = exp2f(ms - M);
     L += w * ps[kHeads + h];
     const float4* po = reinterpret_cast<const float4*>(ps + 2 * kHeads + h * kDim + d0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float4 v = po[i];
-      acc[4 * i + 0] += w * v.x;
-      acc[4 * i + 1] += w * v.y;
-      acc[4 * i + 2] += w * v.z;
-      acc[4 * i + 3] += w * v.w;
-    }
+    const float4 v0 = po[0];
+    const float4 v1 = po[1];
+    acc[0] += w * v0.x;
+    acc[1] += w * v0.y;
+    acc[2] += w * v0.z;
+    acc[3] += w * v0.w;
+    acc[4] += w * v1.x;
+    acc[5] += w * v1.y;
+    acc[6] += w * v1.z;
+    acc[7] += w * v1.w;
   }
   const float sink2 = p.sink[h] * kLog2e;
   const float m_tot = fmaxf(M, sink2);
   const float a = exp2f(M - m_tot);
   const float f = a / (a * L + exp2f(sink2 - m_tot));
-  __bf16* orow = p.o + bi * p.so_b + mi * p.so_m + int64_t(h) * p.so_h + d0;
+  bf16x8 v;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    bf16x8 v;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = static_cast<__bf16>(acc[8 * i + k] * f);
-    *reinterpret_cast<bf16x8*>(orow + 8 * i) = v;
-  }
+  for (int k = 0; k < 8; ++k) v[k] = static_cast<__bf16>(acc[k] * f);
+  *reinterpret_cast<bf16x8*>(p.o + bi * p.so_b + mi * p.so_m + int64_t(h) * p.so_h + d0) = v;
 }
 
 // Compute units of the current device, cached per device ordinal.
@@ -415,7 +848,7 @@ int sa_abi_version(void) { return SA_ABI_VERSION; }
 const char* sa_strerror(int code) {
   switch (code) {
     case SA_OK: return "ok";
-    case SA_EINVAL: return "invalid argument (null pointer, size, stride or alignment)";
+    case SA_EINVAL: return "invalid argument (null pointer, size, stride, alignment or flags)";
     case SA_EUNSUPPORTED: return "unsupported shape (needs h == 16, d == 512)";
     case SA_EWORKSPACE: return "workspace missing or too small";
     case SA_EHIP: return "HIP runtime error";
@@ -447,6 +880,8 @@ int sa_forward(const sa_args* a, void* hip_stream) {
   if (plan.ws_bytes > 0 && (a->workspace == nullptr || a->workspace_bytes < plan.ws_bytes))
     return SA_EWORKSPACE;
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+  const float scale_log2 = a->scale * kLog2e;
 
   FwdParams p{};
   p.q = static_cast<const __bf16*>(a->q);
@@ -454,7 +889,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
   p.sink = a->sink;
   p.idx = a->idx;
   p.o = static_cast<__bf16*>(a->o);
-  p.part = static_cast<float*>(a->workspace);
+  p.part = plan.nsplit > 1 ? reinterpret_cast<float*>(ws + plan.part_off) : nullptr;
   p.err = a->err_word;
   p.m = a->m;
   p.kv_len = a->kv_len;
@@ -469,12 +904,65 @@ int sa_forward(const sa_args* a, void* hip_stream) {
   p.so_b = a->so[0];
   p.so_m = a->so[1];
   p.so_h = a->so[2];
-  p.scale_log2 = a->scale * kLog2e;
+  p.scale_log2 = scale_log2;
   p.nsplit = plan.nsplit;
   p.split_len = plan.split_len;
   p.nblocks = plan.units * plan.nsplit;
 
-  hipLaunchKernelGGL(sa_fwd_kernel, dim3(unsigned(p.nblocks)), dim3(kThreads), 0, stream, p);
+  if (plan.tiles) {
+    IndexParams ip{};
+    ip.idx = a->idx;
+    ip.err = a->err_word;
+    ip.meta = reinterpret_cast<int32_t*>(ws + plan.meta_off);
+    ip.rows = reinterpret_cast<int32_t*>(ws + plan.rows_off);
+    ip.cnts = reinterpret_cast<uint32_t*>(ws + plan.cnts_off);
+    ip.m = a->m;
+    ip.kv_len = a->kv_len;
+    ip.topk = a->topk;
+    ip.si_b = a->sidx[0];
+    ip.si_m = a->sidx[1];
+    ip.tiles_per_b = plan.tiles_per_b;
+    ip.cap = plan.tile_cap;
+    ip.force = (a->flags & SA_FLAG_FORCE_TILES) ? 1 : 0;
+    const size_t lds = size_t(a->kv_len) * sizeof(uint32_t);
+    if (lds > 65536 &&
+        hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
+      return SA_EHIP;
+    hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), lds,
+                       stream, ip);
+    if (hipGetLastError() != hipSuccess) return SA_EHIP;
+
+    TileParams tp{};
+    tp.q = p.q;
+    tp.kv = p.kv;
+    tp.sink = a->sink;
+    tp.o = p.o;
+    tp.meta = ip.meta;
+    tp.rows = ip.rows;
+    tp.cnts = ip.cnts;
+    tp.m = a->m;
+    tp.cap = plan.tile_cap;
+    tp.tiles_per_b = plan.tiles_per_b;
+    tp.sq_b = p.sq_b;
+    tp.sq_m = p.sq_m;
+    tp.sq_h = p.sq_h;
+    tp.skv_b = p.skv_b;
+    tp.skv_n = p.skv_n;
+    tp.so_b = p.so_b;
+    tp.so_m = p.so_m;
+    tp.so_h = p.so_h;
+    tp.scale_log2 = scale_log2;
+    tp.nblocks = plan.ntiles;
+    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), 0,
+                       stream, tp);
+    if (hipGetLastError() != hipSuccess) return SA_EHIP;
+    p.tile_meta = ip.meta;
+    p.tiles_per_b = plan.tiles_per_b;
+  }
+
+  hipLaunchKernelGGL(sa_fwd_query_kernel, dim3(unsigned(p.nblocks)), dim3(kThreads), 0, stream,
+                     p);
   if (hipGetLastError() != hipSuccess) return SA_EHIP;
   if (plan.nsplit > 1) {
     CombineParams c{};
@@ -486,7 +974,8 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     c.so_m = a->so[1];
     c.so_h = a->so[2];
     c.nsplit = plan.nsplit;
-    hipLaunchKernelGGL(sa_combine_kernel, dim3(unsigned(plan.units)), dim3(256), 0, stream, c);
+    hipLaunchKernelGGL(sa_combine_kernel, dim3(unsigned(plan.units * kHeads)), dim3(64), 0,
+                       stream, c);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
   }
   return SA_OK;

@@ -24,14 +24,19 @@ import threading
 
 import torch
 
-__all__ = ["sparse_attn", "set_index_check", "index_check_enabled", "load_extension",
-           "extension_path"]
+__all__ = ["sparse_attn", "set_index_check", "index_check_enabled", "set_path_flags",
+           "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES"]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 _EXT_PATH = os.path.join(_PKG_DIR, "lib", "sa_torch_ext.so")
 _lock = threading.Lock()
 _loaded = False
 _check = os.environ.get("SPARSE_ATTN_CHECK", "1") != "0"
+_flags = 0
+
+# Kernel-path selection bits, as sa_args.flags in include/sparse_attn.h.
+FLAG_PER_QUERY = 1     # every query gathers its own rows
+FLAG_FORCE_TILES = 2   # every eligible 4-query tile shares its row union
 
 
 def extension_path() -> str:
@@ -64,6 +69,12 @@ def index_check_enabled() -> bool:
     return _check
 
 
+def set_path_flags(flags: int) -> None:
+    """Choose the kernel path (``FLAG_*`` bits; 0 lets the library decide)."""
+    global _flags
+    _flags = int(flags)
+
+
 def sparse_attn(q, kv, attn_sink, topk_idxs, scale):
     """
     Args:
@@ -89,7 +100,7 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, scale):
     sink_c = attn_sink.contiguous()
     idx_c = topk_idxs.contiguous()
     err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
-    o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err)
+    o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags)
     if err is not None and int(err.item()) != 0:
         raise RuntimeError(
             f"sparse_attn: topk_idxs holds an index outside [-1, {kv.shape[1]})")

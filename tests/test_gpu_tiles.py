@@ -1,0 +1,151 @@
+"""GPU parity of the shared-row tile path (index kernel + tile kernel) against
+the float64 oracle and against the per-query path on the same inputs.
+
+Tolerance as in test_gpu_parity: max |err| <= 2e-2, mean |err| <= 2e-3,
+relative RMS <= 5e-3 against float64; exact zeros for all -1 rows.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sparse_attn_fp64
+from test_gpu_parity import DEV, check, config, sampled_check, say
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+PER_QUERY, FORCE_TILES = 1, 2
+
+
+def run(q, kv, sink, idx, scale, flags=0, check_err=True):
+    err = torch.zeros(1, dtype=torch.int32, device=DEV) if check_err else None
+    o = torch.ops.sa_amd.sparse_attn_fwd(q.to(DEV), kv.to(DEV), sink.to(DEV), idx.to(DEV),
+                                         float(scale), err, flags)
+    if err is not None:
+        assert int(err.item()) == 0
+    return o
+
+
+def rand_case(b, m, kv_len, topk, seed, minus1=0.0, sink_std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, m, 16, 512, generator=g).to(torch.bfloat16)
+    kv = torch.randn(b, kv_len, 512, generator=g).to(torch.bfloat16)
+    sink = torch.randn(16, generator=g) * sink_std
+    idx = torch.randint(0, kv_len, (b, m, topk), generator=g, dtype=torch.int32)
+    if minus1:
+        idx[torch.rand(b, m, topk, generator=g) < minus1] = -1
+    return q, kv, sink, idx, wl.SCALE
+
+
+def test_causal_prefill_tiles_vs_per_query(gpu_sa):
+    """Full config through both paths: sampled oracle check of the default
+    (tile) path, and every query of the two paths against each other."""
+    q, kv, sink, idx, sc = config("causal_prefill")
+    o_t = run(q, kv, sink, idx, sc)
+    o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY)
+    ts = [0, 1, 2, 3, 4, 5, 6, 7, 2044, 2045, 2046, 2047, 2048, 2049, 4092, 4093, 4094, 4095]
+    ts += torch.randint(0, 4096, (30,), generator=torch.Generator().manual_seed(9)).tolist()
+    sampled_check(o_t, q, kv, sink, idx, sc, [(0, t) for t in ts], "causal tiles")
+    d = (o_t.float() - o_p.float()).abs()
+    say(f"  tiles vs per-query: max {d.max().item():.3e} mean {d.mean().item():.3e}")
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
+
+
+def test_high_locality_tiles_vs_per_query(gpu_sa):
+    q, kv, sink, idx, sc = config("high_locality")
+    o_t = run(q, kv, sink, idx, sc)
+    o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY)
+    d = (o_t.float() - o_p.float()).abs()
+    say(f"  tiles vs per-query: max {d.max().item():.3e} mean {d.mean().item():.3e}")
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
+    sel = [(0, 0), (0, 1), (1, 2), (2, 3), (3, 508), (3, 511)]
+    sampled_check(o_t, q, kv, sink, idx, sc, sel, "high locality tiles")
+
+
+@pytest.mark.parametrize("m", [4, 5, 6, 7, 8, 13])
+def test_forced_tiles_ragged_m(gpu_sa, m):
+    q, kv, sink, idx, sc = rand_case(2, m, 300, 64, seed=100 + m, minus1=0.2)
+    o = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
+    check(o, sparse_attn_fp64(q, kv, sink, idx, sc), f"forced tiles m={m}")
+
+
+def test_forced_tiles_many_queries_long_topk(gpu_sa):
+    # 260 queries >= CUs: no split, so topk > 64 can take the tile path
+    q, kv, sink, idx, sc = rand_case(1, 260, 5000, 700, seed=7, minus1=0.1)
+    o = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
+    sel = [(0, m) for m in (0, 1, 2, 3, 100, 255, 256, 257, 258, 259)]
+    sampled_check(o, q, kv, sink, idx, sc, sel, "forced tiles topk=700")
+    o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY)
+    assert (o.float() - o_p.float()).abs().max().item() <= 2e-2
+
+
+def test_tile_duplicates_multiplicity(gpu_sa):
+    """Duplicates inside a query and shared rows across queries of a tile."""
+    q, kv, sink, idx, sc = rand_case(1, 8, 40, 64, seed=21)  # 64 draws from 40 rows
+    idx[0, 0, :32] = 5       # one row 32 times
+    idx[0, 1, ::2] = 7
+    idx[0, 2] = 9            # every slot the same row: 64-fold
+    o = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
+    check(o, sparse_attn_fp64(q, kv, sink, idx, sc), "tile duplicates")
+
+
+def test_tile_count_overflow_falls_back(gpu_sa):
+    """A row repeated more than 255 times in one query cannot be counted in a
+    byte; that tile runs per query and stays exact."""
+    q, kv, sink, idx, sc = rand_case(1, 300, 50, 300, seed=22)
+    idx[0, 1] = 3            # 300 copies
+    o = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
+    sel = [(0, 0), (0, 1), (0, 2), (0, 3), (0, 4), (0, 299)]
+    sampled_check(o, q, kv, sink, idx, sc, sel, "count overflow")
+
+
+def test_tile_all_masked_queries(gpu_sa):
+    q, kv, sink, idx, sc = rand_case(1, 12, 100, 64, seed=23, minus1=0.3)
+    idx[0, 4:8] = -1         # a whole tile without valid slots
+    idx[0, 9] = -1           # one all -1 query inside a tile
+    o = run(q, kv, sink, idx, sc, flags=FORCE_TILES).cpu()
+    assert torch.all(o[0, 4:8] == 0) and torch.all(o[0, 9] == 0)
+    check(o, sparse_attn_fp64(q, kv, sink, idx, sc), "masked tiles")
+
+
+def test_tile_largest_count_table(gpu_sa):
+    """kv_len = 32768 needs the 128 KiB count table (dynamic LDS)."""
+    q, kv, sink, idx, sc = rand_case(1, 8, 32768, 64, seed=24)
+    idx[0, :, :32] = torch.arange(32768 - 32, 32768, dtype=torch.int32)  # top rows, shared
+    o = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
+    check(o, sparse_attn_fp64(q, kv, sink, idx, sc), "kv_len 32768 tiles")
+
+
+def test_tile_out_of_range_reported(gpu_sa):
+    q, kv, sink, idx, sc = rand_case(1, 8, 100, 64, seed=25)
+    idx[0, 5, 10] = 100
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    o = torch.ops.sa_amd.sparse_attn_fwd(q.to(DEV), kv.to(DEV), sink.to(DEV), idx.to(DEV),
+                                         sc, err, FORCE_TILES)
+    assert int(err.item()) == 1
+    fixed = idx.clone()
+    fixed[0, 5, 10] = -1
+    check(o, sparse_attn_fp64(q, kv, sink, fixed, sc), "tile bad index skipped")
+
+
+def test_tile_sink_visible_and_exact_rows(gpu_sa):
+    """q = 0, sink = -inf and a 4-query tile sharing rows: every query's output
+    is exactly the mean of its rows when the rows are duplicates of one row."""
+    _, kv, _, _, sc = rand_case(1, 1, 64, 1, seed=26)
+    q = torch.zeros(1, 4, 16, 512, dtype=torch.bfloat16)
+    sink = torch.full((16,), float("-inf"))
+    idx = torch.full((1, 4, 8), -1, dtype=torch.int32)
+    idx[0, 0, 0] = 11
+    idx[0, 1, [1, 2]] = 11        # same row twice
+    idx[0, 2, [0, 3, 5, 7]] = 30  # another row four times
+    idx[0, 3, 4] = 30
+    o = run(q, kv, sink, idx, sc, flags=FORCE_TILES).cpu()
+    for mi, r in ((0, 11), (1, 11), (2, 30), (3, 30)):
+        assert torch.equal(o[0, mi], kv[0, r].expand(16, -1)), mi
+
+
+def test_tiles_deterministic(gpu_sa):
+    q, kv, sink, idx, sc = rand_case(1, 260, 2000, 256, seed=27)
+    a = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
+    b = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
+    assert torch.equal(a, b)

@@ -31,6 +31,7 @@ class SaArgs(ctypes.Structure):
         ("sidx", ctypes.c_int64 * 3), ("so", ctypes.c_int64 * 4),
         ("scale", ctypes.c_float), ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t), ("err_word", ctypes.c_void_p),
+        ("flags", ctypes.c_uint32),
     ]
 
 
@@ -55,6 +56,8 @@ def libs():
                                            ctypes.POINTER(ctypes.c_size_t)]
         lib.sa_strerror.restype = ctypes.c_char_p
     host.sa_host_validate.argtypes = [ctypes.POINTER(SaArgs)]
+    host.sa_host_plan_full.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_int64)]
     host.sa_host_plan.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_int,
                                   ctypes.POINTER(ctypes.c_int64),
                                   ctypes.POINTER(ctypes.c_int64),
@@ -113,7 +116,7 @@ def test_forward_rejects_null_args(libs):
     ("q", 0, SA_EINVAL), ("o", 0, SA_EINVAL), ("sink", 0, SA_EINVAL),
     ("idx", 0, SA_EINVAL), ("kv", 0, SA_EINVAL),
     ("q", 0x10008, SA_EINVAL), ("o", 0x50002, SA_EINVAL), ("kv", 0x20004, SA_EINVAL),
-    ("scale", float("nan"), SA_EINVAL),
+    ("scale", float("nan"), SA_EINVAL), ("flags", 4, SA_EINVAL), ("flags", 1 << 31, SA_EINVAL),
 ])
 def test_forward_argument_errors(libs, field, value, code):
     hip, host = libs
@@ -165,6 +168,37 @@ def plan(host, a, cus):
 PART_BYTES = 2 * 16 * 4 + 16 * 512 * 4
 
 
+def plan_full(host, a, cus):
+    out = (ctypes.c_int64 * 7)()
+    assert host.sa_host_plan_full(ctypes.byref(a), cus, out) == SA_OK
+    keys = ["nsplit", "split_len", "tiles", "tiles_per_b", "ntiles", "tile_cap", "ws"]
+    return dict(zip(keys, list(out)))
+
+
+@pytest.mark.parametrize("b,m,kv_len,topk,flags,tiles", [
+    (1, 4096, 4096, 2048, 0, True),      # causal prefill: shared-row tiles
+    (4, 512, 16384, 512, 0, True),       # high locality
+    (1, 1024, 131072, 2048, 0, False),   # long context: count table too big
+    (32, 1, 32768, 2048, 0, False),      # decode: one query per batch, split
+    (1, 4096, 4096, 2048, 1, False),     # SA_FLAG_PER_QUERY
+    (1, 8, 32768, 64, 2, True),          # largest count table, no split
+    (1, 8, 32769, 64, 2, False),
+    (1, 3, 100, 64, 2, False),           # fewer queries than a tile
+    (1, 300, 100, 0, 0, False),          # no slots
+])
+def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
+    _, host = libs
+    a = good_args(b=b, m=m, topk=topk, kv_len=kv_len)
+    a.flags = flags
+    p = plan_full(host, a, 256)
+    assert bool(p["tiles"]) == tiles
+    if tiles:
+        assert p["nsplit"] == 1
+        assert p["tiles_per_b"] == -(-m // 4) and p["ntiles"] == b * p["tiles_per_b"]
+        assert p["tile_cap"] % 64 == 0 and p["tile_cap"] >= min(kv_len, 4 * topk)
+        assert p["ws"] >= p["ntiles"] * (16 + 8 * p["tile_cap"])
+
+
 @pytest.mark.parametrize("b,m,topk,cus,expect_ns,expect_len", [
     (32, 1, 2048, 256, 8, 256),      # decode: 32 queries -> 8 parts of 4 tiles
     (1, 4096, 2048, 256, 1, 2048),   # causal prefill: enough queries
@@ -181,7 +215,8 @@ def test_split_plan(libs, b, m, topk, cus, expect_ns, expect_len):
     ns, sl, ws = plan(host, a, cus)
     assert (ns, sl) == (expect_ns, expect_len)
     assert (ns - 1) * sl < topk <= ns * sl           # parts cover topk exactly
-    assert ws == (0 if ns == 1 else b * m * ns * PART_BYTES)
+    if ns > 1:
+        assert ws == b * m * ns * PART_BYTES
 
 
 def test_python_dropin_refuses_cpu_tensors():
