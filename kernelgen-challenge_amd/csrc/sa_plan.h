@@ -17,9 +17,9 @@ constexpr int64_t kMaxUnits = int64_t(1) << 24;  // work-groups per launch
 
 // Shared-row tiles: kTileQueries consecutive queries of one batch gather the
 // union of their rows once. The union is built from a per-row count table in
-// LDS, so it needs kv_len <= kMaxTileKv.
-constexpr int kTileQueries = 4;
-constexpr int64_t kMaxTileKv = 32768;
+// LDS (one byte per query, 8 bytes per row), so it needs kv_len <= kMaxTileKv.
+constexpr int kTileQueries = 8;
+constexpr int64_t kMaxTileKv = 16384;
 
 // Tile modes written by the index kernel.
 constexpr int kModePerQuery = 0;
@@ -40,7 +40,8 @@ struct Plan {
   bool tiles;          // shared-row path enabled
   int64_t tiles_per_b; // ceil(m / kTileQueries)
   int64_t ntiles;      // b * tiles_per_b
-  int64_t tile_cap;    // union entries stored per tile (multiple of kTileRows)
+  int64_t tile_cap;    // union entries stored per tile (multiple of kTileRows);
+                       // each has an int32 row and kTileQueries count bytes
   size_t meta_off, rows_off, cnts_off, part_off;  // workspace byte offsets
   size_t ws_bytes;     // total workspace
 };
@@ -120,7 +121,7 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     p.split_len = a->topk;
   }
   p.tiles = p.nsplit == 1 && (a->flags & SA_FLAG_PER_QUERY) == 0 &&
-            a->m >= kTileQueries && a->topk > 0 && a->kv_len > 0 &&
+            a->m >= kTileQueries / 2 && a->topk > 0 && a->kv_len > 0 &&
             a->kv_len <= kMaxTileKv;
   size_t off = 0;
   if (p.tiles) {
@@ -133,7 +134,7 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     p.rows_off = off;
     off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
     p.cnts_off = off;
-    off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
+    off = round_up(off + size_t(p.ntiles) * p.tile_cap * kTileQueries, 256);
   }
   if (p.nsplit > 1) {
     p.part_off = off;

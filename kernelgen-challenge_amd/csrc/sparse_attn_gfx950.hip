@@ -66,14 +66,20 @@ constexpr float kLog2e = 1.4426950408889634f;
 // when a tile's max exceeds it by more than this (log2 units), so exp2(s - m)
 // stays below 2^8 and the accumulators are rescaled rarely.
 constexpr float kRescaleLog2 = 8.f;
+// Shared tiles never rescale O: scores may exceed a column's fixed reference
+// by up to this (log2 units; weights <= 255 * 2^24 stay far from fp32 and
+// bf16 overflow). A larger jump sends the tile to the per-query kernel.
+constexpr float kTileMaxJump = 24.f;
 
 constexpr int kTQ = sa::kTileQueries;       // queries per shared tile
-constexpr int kCols = kTQ * kHeads;         // 64 (query, head) columns
-constexpr int kPPitch = kTileRows + 8;      // bf16 per P row in LDS (144 B)
+// A tile is shared when the dense (query x union row) MFMA work is at most
+// this multiple of its valid (query, slot) pairs: gathering every query's rows
+// separately costs about as much per pair as several dense MFMA pairs.
+constexpr int kSharedWaste = 3;
 
 static_assert(kListCap % kThreads == 0, "compaction split");
 static_assert(kRowsPerWave == 16, "one 16-row MFMA block per wave");
-static_assert(kCols == 64 && kTileRows == 64, "shared tile wave layout");
+static_assert(kTQ == 2 * kWaves && kTileRows == 64, "shared tile wave layout");
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
@@ -109,7 +115,7 @@ struct IndexParams {
   int32_t* err;
   int32_t* meta;        // [ntiles][kMetaInts]
   int32_t* rows;        // [ntiles][cap]
-  uint32_t* cnts;       // [ntiles][cap], byte q = multiplicity in query q
+  uint8_t* cnts;        // [ntiles][cap / 64][kTQ][64] multiplicity bytes
   int64_t m, kv_len, topk;
   int64_t si_b, si_m;
   int64_t tiles_per_b, cap;
@@ -122,8 +128,9 @@ struct TileParams {
   const float* sink;
   __bf16* o;
   const int32_t* meta;
+  int32_t* meta_out;    // same array: a tile that must rescale marks itself per-query
   const int32_t* rows;
-  const uint32_t* cnts;
+  const uint8_t* cnts;
   int64_t m, cap, tiles_per_b;
   int64_t sq_b, sq_m, sq_h;
   int64_t skv_b, skv_n;
@@ -163,6 +170,23 @@ __device__ __forceinline__ bf16x4 lds_read_tr16(const uint8_t* p) {
 // lds + lane * 16 (or 4); `lds` must be wave-uniform.
 __device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
   __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)((lds_u8_t*)(lds)), 16, 0, 0);
+}
+
+// The same 16-byte LDS-DMA issued from inline assembly, for pipelines that
+// read one LDS buffer while gathering into another: the compiler does not see
+// this as an LDS write, so it does not wait for the gather before every LDS
+// read. The caller must wait (vmcnt = 0, e.g. dma_barrier()) before any wave
+// reads the destination.
+__device__ __forceinline__ void lds_dma16_async(const void* gsrc, void* lds) {
+  const uint32_t lds_addr =
+      __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>((lds_u8_t*)(lds))));
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(gsrc), "s"(lds_addr)
+      : "memory", "m0");
 }
 
 __device__ __forceinline__ void lds_dma4(const void* gsrc, void* lds) {
@@ -427,8 +451,11 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdPara
 // ============================================================================
 // tile index kernel
 // ============================================================================
+// Count layout of a tile: for step s (64 union entries) and tile query q, the
+// 64 count bytes of the step's rows are contiguous at ((s * kTQ) + q) * 64, so
+// a lane reads the counts of 4 consecutive rows of its query as one dword.
 __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexParams p) {
-  extern __shared__ uint32_t s_count[];  // [kv_len], byte q = count in query q
+  extern __shared__ unsigned long long s_count[];  // [kv_len], byte q = count in query q
   __shared__ int s_wtot[kWaves];
   __shared__ int s_nv[kTQ];
   __shared__ int s_bsum[kTQ];
@@ -443,7 +470,7 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
   const int qt = int(min(int64_t(kTQ), p.m - q0));
   const int kvl = int(p.kv_len);
 
-  for (int i = tid; i < kvl; i += kThreads) s_count[i] = 0u;
+  for (int i = tid; i < kvl; i += kThreads) s_count[i] = 0ull;
   if (tid < kTQ) {
     s_nv[tid] = 0;
     s_bsum[tid] = 0;
@@ -458,7 +485,7 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
     for (int64_t t = tid; t < p.topk; t += kThreads) {
       const int v = irow[t];
       if (v >= 0 && v < kvl) {
-        atomicAdd(&s_count[v], 1u << (8 * qq));
+        atomicAdd(&s_count[v], 1ull << (8 * qq));
         ++nv;
       } else if (v != -1) {
         bad = true;
@@ -475,15 +502,17 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
   const int lo = min(kvl, tid * chunk);
   const int hi = min(kvl, lo + chunk);
   int c = 0;
-  int bsum[kTQ] = {0, 0, 0, 0};
+  int bsum[kTQ];
+#pragma unroll
+  for (int k = 0; k < kTQ; ++k) bsum[k] = 0;
   int first = kvl;
   for (int i = lo; i < hi; ++i) {
-    const uint32_t w = s_count[i];
-    if (w != 0u) {
+    const unsigned long long w = s_count[i];
+    if (w != 0ull) {
       if (c == 0) first = i;
       ++c;
 #pragma unroll
-      for (int k = 0; k < kTQ; ++k) bsum[k] += int((w >> (8 * k)) & 255u);
+      for (int k = 0; k < kTQ; ++k) bsum[k] += int((w >> (8 * k)) & 255ull);
     }
   }
   int incl = c;
@@ -510,21 +539,20 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
     nU += t;
   }
   int32_t* rows = p.rows + tile * p.cap;
-  uint32_t* cnts = p.cnts + tile * p.cap;
+  uint8_t* cnts = p.cnts + tile * p.cap * kTQ;
+  auto put = [&](int e, int row, unsigned long long w) {
+    rows[e] = row;
+    uint8_t* cb = cnts + (e / kTileRows) * (kTQ * kTileRows) + (e % kTileRows);
+#pragma unroll
+    for (int k = 0; k < kTQ; ++k) cb[k * kTileRows] = uint8_t((w >> (8 * k)) & 255ull);
+  };
   for (int i = lo; i < hi; ++i) {
-    const uint32_t w = s_count[i];
-    if (w != 0u) {
-      rows[pos] = i;
-      cnts[pos] = w;
-      ++pos;
-    }
+    const unsigned long long w = s_count[i];
+    if (w != 0ull) put(pos++, i, w);
   }
   // pad to whole 64-row steps with a valid row of count 0
   const int padded = (nU + kTileRows - 1) / kTileRows * kTileRows;
-  for (int i = nU + tid; i < padded; i += kThreads) {
-    rows[i] = s_first;
-    cnts[i] = 0u;
-  }
+  for (int e = nU + tid; e < padded; e += kThreads) put(e, s_first, 0ull);
   if (tid == 0) {
     bool overflow = false;
     int total = 0;
@@ -532,8 +560,10 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
       overflow |= s_bsum[k] != s_nv[k];  // a count passed 255 and carried
       total += s_nv[k];
     }
+    // shared when the dense (query x union row) work is at most
+    // kSharedWaste times the valid slots
     const bool shared =
-        !overflow && (p.force != 0 || int64_t(qt) * nU <= 2 * int64_t(total));
+        !overflow && (p.force != 0 || int64_t(qt) * nU <= kSharedWaste * int64_t(total));
     int32_t* meta = p.meta + tile * kMetaInts;
     meta[0] = nU;
     meta[1] = shared ? kModeShared : sa::kModePerQuery;
@@ -545,22 +575,33 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
 // ============================================================================
 // shared-row tile kernel
 // ============================================================================
-// Waves: w = 2c + r. For S^T, wave (r, c) owns union rows 32r..32r+31 of the
-// step and the 32 columns of queries 2c, 2c+1 (Q^T of those two queries is
-// resident: 32 k-steps of 16 d). For O, wave w owns d = 128w .. 128w+127 for
-// all 64 columns (2 x 4 blocks of 32 x 32 fp32 accumulators).
+// LDS row layout: a gathered row is 1 KiB stored at a 1040-byte pitch. The
+// 16-byte shift per row spreads the ds_read_b128 K reads of 16 consecutive
+// rows over all 64 banks, and every K/V read of a lane is its base address
+// plus a compile-time offset.
+constexpr int kTilePitch = kRowBytes + 16;
+
+// Each wave owns two queries of the tile outright: their Q^T (128 VGPRs),
+// their O[32 columns x 512 d] (16 blocks of 32 x 32 fp32, in AGPRs), their
+// softmax state and P. The four waves share only the gathered rows, so the
+// one barrier per step is the gather's.
+//   S^T block rb (rows 32rb..32rb+31 of the step) x the wave's 32 columns:
+//     lane (l32, hi) holds column l32 (query 2w + l32/16, head l32 % 16) and
+//     rows 32rb + 8a + 4hi + b in register 4a + b.
+//   PV k-block kb (16 rows) takes k-group hi = rows 16kb + 4hi + (0..3) and
+//     16kb + 8 + 4hi + (0..3): exactly this lane's S^T registers, so P feeds
+//     the MFMA A operand without leaving registers.
+//   O block nb: column n < 16 is d = 128(nb/4) + 16(nb%4) + n, column n >= 16
+//     is d = 128(nb/4) + 64 + 16(nb%4) + n - 16; rows are the 32 (query, head)
+//     columns in the S^T register order.
 __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kRowStride];
-  __shared__ __attribute__((aligned(16))) __bf16 s_p[kCols * kPPitch];
-  __shared__ __attribute__((aligned(16))) uint32_t s_cnt[2][kTileRows];
-  __shared__ __attribute__((aligned(16))) float s_red[2][kCols];
-  __shared__ __attribute__((aligned(16))) float s_alpha[kCols];
+  __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kTilePitch];
+  __shared__ __attribute__((aligned(16))) uint8_t s_cnt[2][kTQ * kTileRows];
+  __shared__ int s_abort;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = wave & 1;
-  const int c = wave >> 1;
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
@@ -571,14 +612,26 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   const int64_t bi = tile / p.tiles_per_b;
   const int64_t q0 = (tile % p.tiles_per_b) * kTQ;
   const int qt = int(min(int64_t(kTQ), p.m - q0));
+  const int nsteps = (nU + kTileRows - 1) / kTileRows;
+  if (nsteps == 0) {
+    // no valid slot in any query of the tile: the sink takes all the mass
+    __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m;
+    for (int i = tid; i < qt * kHeads * (kDim / 8); i += kThreads) {
+      const int qh = i / (kDim / 8);
+      bf16x8 z;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) z[e] = static_cast<__bf16>(0.f);
+      *reinterpret_cast<bf16x8*>(ob + int64_t(qh >> 4) * p.so_m + int64_t(qh & 15) * p.so_h +
+                                 8 * (i % (kDim / 8))) = z;
+    }
+    return;
+  }
 
-  // this lane's S^T column: query qq of the tile, head hh
-  const int col = 32 * c + l32;
-  const int qq = 2 * c + (l32 >> 4);
-  const int hh = l32 & 15;
+  const int qw = 2 * wave + (l32 >> 4);  // this lane's query within the tile
+  const int hh = l32 & 15;                // and head
   bf16x8 qf[kDim / 16];
-  if (qq < qt) {
-    const __bf16* qrow = p.q + bi * p.sq_b + (q0 + qq) * p.sq_m + int64_t(hh) * p.sq_h + 8 * hi;
+  if (qw < qt) {
+    const __bf16* qrow = p.q + bi * p.sq_b + (q0 + qw) * p.sq_m + int64_t(hh) * p.sq_h + 8 * hi;
 #pragma unroll
     for (int s = 0; s < kDim / 16; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
   } else {
@@ -589,184 +642,215 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   }
 
   const int32_t* urows = p.rows + tile * p.cap;
-  const uint32_t* ucnts = p.cnts + tile * p.cap;
+  const uint8_t* ucnts = p.cnts + tile * p.cap * kTQ;
   const __bf16* kvb = p.kv + bi * p.skv_b;
-  const int nsteps = (nU + kTileRows - 1) / kTileRows;
 
-  // Union rows of a step: lane i (< 16) of wave w holds row 16w + i; the
-  // gather reads them back with readlane so its addresses are scalar.
+  // Union rows of a step: lane i (< 16) of wave w holds row 16w + i. The
+  // gather reads them back with readlane, so its row addresses are scalar.
   auto step_rows = [&](int step) -> int {
     return urows[step * kTileRows + wave * kRowsPerWave + (lane & 15)];
   };
-  auto fetch = [&](int rows_v, int step, int buf) {
-#pragma unroll
-    for (int i = 0; i < kRowsPerWave; ++i) {
-      const int row = __builtin_amdgcn_readlane(rows_v, i);
-      lds_dma16(kvb + int64_t(row) * p.skv_n + 8 * lane,
-                &s_tile[buf][(wave * kRowsPerWave + i) * kRowStride]);
-    }
-    if (wave == 0) lds_dma4(ucnts + step * kTileRows + lane, &s_cnt[buf][0]);
+  // One 1 KiB row into LDS row 16w + i (lane l moves bytes 16l..16l+15).
+  auto dma_row = [&](int rows_v, int i, int buf) {
+    const int row = __builtin_amdgcn_readlane(rows_v, i);
+    lds_dma16_async(kvb + int64_t(row) * p.skv_n + 8 * lane,
+                    &s_tile[buf][(wave * kRowsPerWave + i) * kTilePitch]);
+  };
+  // The 512 count bytes of a step (wave 0, lanes 0..31).
+  auto dma_counts = [&](int step, int buf) {
+    if (wave == 0 && lane < 32)
+      lds_dma16_async(ucnts + step * (kTQ * kTileRows) + 16 * lane, &s_cnt[buf][0]);
   };
 
-  float m_run = -INFINITY;  // running max of column `col` (log2 domain)
+  float m_run = -INFINITY;  // reference max of column l32 (log2 domain)
   float l_run = 0.f;        // this lane's share of the column's sum
-  f32x16 oacc[2][4];
+  f32x16 oacc[kDim / 32];
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
+  for (int nb = 0; nb < kDim / 32; ++nb) {
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) oacc[mb][nb][i] = 0.f;
+    for (int i = 0; i < 16; ++i) oacc[nb][i] = 0.f;
+    asm volatile("" : "+a"(oacc[nb]));  // O lives in AGPRs (MFMA C/D only)
+  }
 
-  int rows_next = 0;
-  if (nsteps > 0) fetch(step_rows(0), 0, 0);
-  if (nsteps > 1) rows_next = step_rows(1);
+  {
+    const int rv = step_rows(0);
+#pragma unroll
+    for (int i = 0; i < kRowsPerWave; ++i) dma_row(rv, i, 0);
+    dma_counts(0, 0);
+  }
+  int rows_next = step_rows(min(1, nsteps - 1));
+  if (tid == 0) s_abort = 0;
   dma_barrier();
+
+  // K operand: lane reads row 32rb + l32, bytes 32s + 16hi.
+  const int koff = l32 * kTilePitch + 16 * hi;
+  // V operand: 16-lane group G reads rows 16kb + 4(G>>1) + j/4 (and + 8),
+  // bytes 2 * (64(G&1) + 4(j&3)) of each 32-column block.
+  const int G = lane >> 4;
+  const int j = lane & 15;
+  const int voff = (4 * (G >> 1) + (j >> 2)) * kTilePitch + 128 * (G & 1) + 8 * (j & 3);
 
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
-    if (step + 1 < nsteps) {
-      fetch(rows_next, step + 1, buf ^ 1);
-      if (step + 2 < nsteps) rows_next = step_rows(step + 2);
-    }
     const uint8_t* tb = s_tile[buf];
+    const uint8_t* cb = s_cnt[buf];
+    const int nxt = min(step + 1, nsteps - 1);  // the last step refetches itself: harmless
 
-    // ---- S^T[rows 32r.., cols 32c..] = K . Q^T ---------------------------------
-    f32x16 sacc;
+    // ---- S^T = K . Q^T for both row blocks; next step's rows 0..7 gathered ----
+    // One k-step (2 MFMAs) per group; K fragments are read two groups ahead
+    // into a 3-slot register ring so LDS latency hides behind the MFMAs.
+    f32x16 sacc[2];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) sacc[i] = 0.f;
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[rb][i] = 0.f;
     {
-      // K fragments are read 4 k-steps ahead of the MFMA that uses them
-      const uint8_t* krow = tb + (32 * r + l32) * kRowStride + 16 * hi;
-      bf16x8 kf[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 32 * s);
+      const uint8_t* kr0 = tb + koff;
+      const uint8_t* kr1 = kr0 + 32 * kTilePitch;
+      bf16x8 kf[3][2];
+      auto kread = [&](int s, int slot) {
+        kf[slot][0] = *reinterpret_cast<const bf16x8*>(kr0 + 32 * s);
+        kf[slot][1] = *reinterpret_cast<const bf16x8*>(kr1 + 32 * s);
+      };
+      kread(0, 0);
+      kread(1, 1);
 #pragma unroll
       for (int s = 0; s < kDim / 16; ++s) {
-        const bf16x8 cur = kf[s & 3];
-        if (s + 4 < kDim / 16) kf[s & 3] = *reinterpret_cast<const bf16x8*>(krow + 32 * (s + 4));
-        sacc = mfma_32x32x16(cur, qf[s], sacc);
+        if (s + 2 < kDim / 16) kread(s + 2, (s + 2) % 3);
+        sacc[0] = mfma_32x32x16(kf[s % 3][0], qf[s], sacc[0]);
+        sacc[1] = mfma_32x32x16(kf[s % 3][1], qf[s], sacc[1]);
+        if ((s & 3) == 3) dma_row(rows_next, s >> 2, buf ^ 1);
+        __builtin_amdgcn_sched_barrier(0);  // keep the read-ahead order
       }
     }
-    // lane holds column `col`, rows 32r + 8a + 4hi + b for register 4a + b
+    // S^T goes to VALU next: keep it in VGPRs (AGPRs hold O)
+    asm volatile("" : "+v"(sacc[0]), "+v"(sacc[1]));
 
-    // ---- multiplicity, masking and the column max -------------------------------
-    // count c of each row in this lane's query: p = c * 2^(s - m), c = 0 masks
-    const int qshift = 8 * qq;
-    float sv[16];
+    // counts of this lane's rows in its query: rows 32rb + 8a + 4hi + (0..3)
+    uint32_t cw[2][4];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        cw[rb][a] = *reinterpret_cast<const uint32_t*>(
+            &cb[qw * kTileRows + 32 * rb + 8 * a + 4 * hi]);
+
+    // ---- masking, column max over the step's 64 rows, lazy rescale ---------------
     float mx = -INFINITY;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const uint4 w4 = *reinterpret_cast<const uint4*>(&s_cnt[buf][32 * r + 8 * a + 4 * hi]);
-      const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const bool valid = ((ws[b] >> qshift) & 255u) != 0u;
-        sv[4 * a + b] = valid ? sacc[4 * a + b] * p.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sv[4 * a + b]);
-      }
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const bool valid = ((cw[rb][a] >> (8 * b)) & 255u) != 0u;
+          const float s = valid ? sacc[rb][4 * a + b] * p.scale_log2 : -INFINITY;
+          sacc[rb][4 * a + b] = s;
+          mx = fmaxf(mx, s);
+        }
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                       false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // -inf: no row this step
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    if (hi == 0) s_red[r][col] = mx;
-    lds_barrier();
-    const float mstep = fmaxf(s_red[0][col], s_red[1][col]);  // -inf: no row of this step
-    float alpha = 1.f;
-    if (mstep > m_run + kRescaleLog2) {
-      alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mstep);  // O, l still 0 at first
-      m_run = mstep;
-    }
+    // Fixed reference: a column keeps the max of its first non-empty step. A
+    // later step more than kTileMaxJump above it would need O rescaled; the
+    // tile then hands itself to the per-query kernel (which rescales online).
+    if (__any(m_run != -INFINITY && mx > m_run + kTileMaxJump)) s_abort = 1;
+    if (m_run == -INFINITY) m_run = mx;
     const float mref = m_run == -INFINITY ? 0.f : m_run;  // column still empty
     float psum = 0.f;
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const uint4 w4 = *reinterpret_cast<const uint4*>(&s_cnt[buf][32 * r + 8 * a + 4 * hi]);
-      const uint32_t ws[4] = {w4.x, w4.y, w4.z, w4.w};
-      bf16x4 pb;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const float cnt = float((ws[b] >> qshift) & 255u);
-        const float pj = cnt * exp2f(sv[4 * a + b] - mref);
-        psum += pj;
-        pb[b] = static_cast<__bf16>(pj);
-      }
-      *reinterpret_cast<bf16x4*>(&s_p[col * kPPitch + 32 * r + 8 * a + 4 * hi]) = pb;
-    }
-    l_run = l_run * alpha + psum;
-    if (r == 0 && hi == 0) s_alpha[col] = alpha;
-    lds_barrier();
 
-    // ---- O[:, 128w..] = alpha * O + P . V --------------------------------------
+    // ---- O += P . V over 4 k-blocks of 16 rows; next step's rows 8..15 gathered ----
+    // P of k-block kb (bf16 A operand) straight from this lane's S^T registers.
+    auto make_pa = [&](int kb) -> bf16x8 {
+      const int rb = kb >> 1;
+      const int a0 = 2 * (kb & 1);
+      bf16x8 pa;
 #pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      float al[16];
-      bool any = false;
-#pragma unroll
-      for (int a = 0; a < 4; ++a) {
-        const float4 a4 = *reinterpret_cast<const float4*>(&s_alpha[32 * mb + 8 * a + 4 * hi]);
-        al[4 * a + 0] = a4.x;
-        al[4 * a + 1] = a4.y;
-        al[4 * a + 2] = a4.z;
-        al[4 * a + 3] = a4.w;
-        any |= (a4.x != 1.f) | (a4.y != 1.f) | (a4.z != 1.f) | (a4.w != 1.f);
+      for (int e = 0; e < 8; ++e) {
+        const int a = a0 + (e >> 2);
+        const int b = e & 3;
+        const float cnt = float((cw[rb][a] >> (8 * b)) & 255u);
+        const float pj = cnt * exp2f(sacc[rb][4 * a + b] - mref);  // c * 2^(s - m)
+        psum += pj;
+        pa[e] = static_cast<__bf16>(pj);
       }
-      if (__any(any)) {
+      return pa;
+    };
+    // Groups of 2 d-blocks (2 MFMAs, 4 transposing reads); V fragments are
+    // read two groups ahead into a 3-slot register ring.
+    {
+      constexpr int kGroups = (kTileRows / 16) * (kDim / 64);  // 4 k-blocks x 8 groups
+      bf16x4 vv[3][4];
+      auto vread = [&](int g, int slot) {
+        const int kb = g >> 3;
+        const uint8_t* v0p = tb + voff + 16 * kb * kTilePitch;
+        const uint8_t* v1p = v0p + 8 * kTilePitch;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb)
+        for (int i = 0; i < 2; ++i) {
+          const int nb = 2 * (g & 7) + i;
+          const int cb2 = 256 * (nb >> 2) + 32 * (nb & 3);  // bytes of d = 128(nb/4) + 16(nb%4)
+          vv[slot][2 * i] = lds_read_tr16(v0p + cb2);
+          vv[slot][2 * i + 1] = lds_read_tr16(v1p + cb2);
+        }
+      };
+      bf16x8 pa = make_pa(0);
+      bf16x8 pa_next = pa;
+      vread(0, 0);
+      vread(1, 1);
 #pragma unroll
-          for (int i = 0; i < 16; ++i) oacc[mb][nb][i] *= al[i];
+      for (int g = 0; g < kGroups; ++g) {
+        const int kb = g >> 3;
+        if (g + 2 < kGroups) vread(g + 2, (g + 2) % 3);
+        if ((g & 7) == 0 && kb + 1 < kTileRows / 16) pa_next = make_pa(kb + 1);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const bf16x4 v0 = vv[g % 3][2 * i];
+          const bf16x4 v1 = vv[g % 3][2 * i + 1];
+          const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+          const int nb = 2 * (g & 7) + i;
+          oacc[nb] = mfma_32x32x16(pa, vf, oacc[nb]);
+        }
+        if ((g & 3) == 3) dma_row(rows_next, 8 + (g >> 2), buf ^ 1);
+        if ((g & 7) == 7) pa = pa_next;
+        __builtin_amdgcn_sched_barrier(0);  // keep the read-ahead order
       }
     }
-    const int G = lane >> 4;
-    const int j = lane & 15;
-#pragma unroll
-    for (int kb = 0; kb < kTileRows / 16; ++kb) {
-      bf16x8 pa[2];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-        pa[mb] = *reinterpret_cast<const bf16x8*>(&s_p[(32 * mb + l32) * kPPitch + 16 * kb + 8 * hi]);
-      const uint8_t* vb = tb + (16 * kb + 8 * (G >> 1) + (j >> 2)) * kRowStride +
-                          (wave * kDPerWave + 16 * (G & 1) + 4 * (j & 3)) * 2;
-#pragma unroll
-      for (int nb = 0; nb < 4; ++nb) {
-        const bf16x4 v0 = lds_read_tr16(vb + nb * 64);
-        const bf16x4 v1 = lds_read_tr16(vb + 4 * kRowStride + nb * 64);
-        const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb) oacc[mb][nb] = mfma_32x32x16(pa[mb], vf, oacc[mb][nb]);
-      }
-    }
+    l_run += psum;
+    dma_counts(nxt, buf ^ 1);
+    rows_next = step_rows(min(step + 2, nsteps - 1));
     dma_barrier();  // every wave's prefetch has landed
+    if (s_abort != 0) {  // uniform: read after the barrier by every wave
+      if (tid == 0) p.meta_out[tile * kMetaInts + 1] = sa::kModePerQuery;
+      return;            // no o written; no transfer in flight
+    }
   }
 
   // ---- epilogue: column sums, sink fold, bf16 store -----------------------------
-  const float lw = l_run + __shfl_xor(l_run, 32);
-  if (hi == 0) s_red[r][col] = lw;
-  __syncthreads();
-  if (r == 0 && hi == 0) {
-    const float lt = s_red[0][col] + s_red[1][col];
+  float f;
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run),
+                                                     __float_as_uint(l_run), false, false);
+    const float lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     const float sink2 = p.sink[hh] * kLog2e;
     const float mt = fmaxf(m_run, sink2);
     const float a = exp2f(m_run - mt);  // 0 when the column has no valid slot
-    s_alpha[col] = a / (a * lt + exp2f(sink2 - mt));
+    f = a / (a * lt + exp2f(sink2 - mt));
   }
-  __syncthreads();
-  __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + wave * kDPerWave + l32;
+  __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + (l32 & 15) + 64 * (l32 >> 4);
 #pragma unroll
-  for (int mb = 0; mb < 2; ++mb)
+  for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const float4 f4 = *reinterpret_cast<const float4*>(&s_alpha[32 * mb + 8 * a + 4 * hi]);
-      const float fs[4] = {f4.x, f4.y, f4.z, f4.w};
+    for (int b = 0; b < 4; ++b) {
+      const int cidx = 8 * a + 4 * hi + b;  // O row = S^T column of the wave
+      const float fs = __shfl(f, cidx);
+      const int q2 = 2 * wave + (cidx >> 4);
+      if (q2 < qt) {
+        __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t(cidx & 15) * p.so_h;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int qh = 32 * mb + 8 * a + 4 * hi + b;
-        const int q2 = qh >> 4;
-        if (q2 < qt) {
-          __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t(qh & 15) * p.so_h;
-#pragma unroll
-          for (int nb = 0; nb < 4; ++nb)
-            orow[32 * nb] = static_cast<__bf16>(oacc[mb][nb][4 * a + b] * fs[b]);
-        }
+        for (int nb = 0; nb < kDim / 32; ++nb)
+          orow[128 * (nb >> 2) + 16 * (nb & 3)] = static_cast<__bf16>(oacc[nb][4 * a + b] * fs);
       }
     }
 }
@@ -915,7 +999,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     ip.err = a->err_word;
     ip.meta = reinterpret_cast<int32_t*>(ws + plan.meta_off);
     ip.rows = reinterpret_cast<int32_t*>(ws + plan.rows_off);
-    ip.cnts = reinterpret_cast<uint32_t*>(ws + plan.cnts_off);
+    ip.cnts = ws + plan.cnts_off;
     ip.m = a->m;
     ip.kv_len = a->kv_len;
     ip.topk = a->topk;
@@ -924,7 +1008,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     ip.tiles_per_b = plan.tiles_per_b;
     ip.cap = plan.tile_cap;
     ip.force = (a->flags & SA_FLAG_FORCE_TILES) ? 1 : 0;
-    const size_t lds = size_t(a->kv_len) * sizeof(uint32_t);
+    const size_t lds = size_t(a->kv_len) * sizeof(unsigned long long);
     if (lds > 65536 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
@@ -939,6 +1023,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     tp.sink = a->sink;
     tp.o = p.o;
     tp.meta = ip.meta;
+    tp.meta_out = ip.meta;
     tp.rows = ip.rows;
     tp.cnts = ip.cnts;
     tp.m = a->m;

@@ -62,7 +62,7 @@ def test_high_locality_tiles_vs_per_query(gpu_sa):
     sampled_check(o_t, q, kv, sink, idx, sc, sel, "high locality tiles")
 
 
-@pytest.mark.parametrize("m", [4, 5, 6, 7, 8, 13])
+@pytest.mark.parametrize("m", [4, 5, 7, 8, 9, 13, 16, 23])
 def test_forced_tiles_ragged_m(gpu_sa, m):
     q, kv, sink, idx, sc = rand_case(2, m, 300, 64, seed=100 + m, minus1=0.2)
     o = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
@@ -89,6 +89,24 @@ def test_tile_duplicates_multiplicity(gpu_sa):
     check(o, sparse_attn_fp64(q, kv, sink, idx, sc), "tile duplicates")
 
 
+def test_tile_reference_jump_falls_back(gpu_sa):
+    """A column whose scores jump far above its first step's max makes the tile
+    hand itself to the per-query kernel (the tile kernel never rescales O):
+    that tile's queries then match the per-query path bit for bit."""
+    q, kv, sink, idx, sc = rand_case(1, 16, 200, 128, seed=28)
+    kv[0, 150] = (q[0, 2].float().mean(0) * 60).to(torch.bfloat16)  # a row matching query 2
+    idx[0, 2, :64] = torch.arange(64, dtype=torch.int32)   # first step: ordinary rows
+    idx[0, 2, 64] = 150                                     # later: a huge score
+    o_t = run(q, kv, sink, idx, sc, flags=FORCE_TILES).cpu()
+    o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY).cpu()
+    assert torch.equal(o_t[0, :8], o_p[0, :8])             # tile 0 ran per query
+    exp = sparse_attn_fp64(q, kv, sink, idx, sc)
+    err = o_t.double().numpy() - exp
+    rel = float(np.sqrt((err ** 2).mean() / (exp ** 2).mean()))
+    say(f"  reference jump: rel_rms={rel:.3e}")
+    assert rel <= 5e-3
+
+
 def test_tile_count_overflow_falls_back(gpu_sa):
     """A row repeated more than 255 times in one query cannot be counted in a
     byte; that tile runs per query and stays exact."""
@@ -101,19 +119,19 @@ def test_tile_count_overflow_falls_back(gpu_sa):
 
 def test_tile_all_masked_queries(gpu_sa):
     q, kv, sink, idx, sc = rand_case(1, 12, 100, 64, seed=23, minus1=0.3)
-    idx[0, 4:8] = -1         # a whole tile without valid slots
-    idx[0, 9] = -1           # one all -1 query inside a tile
+    idx[0, 8:12] = -1        # a whole (ragged) tile without valid slots
+    idx[0, 3] = -1           # one all -1 query inside a tile
     o = run(q, kv, sink, idx, sc, flags=FORCE_TILES).cpu()
-    assert torch.all(o[0, 4:8] == 0) and torch.all(o[0, 9] == 0)
+    assert torch.all(o[0, 8:12] == 0) and torch.all(o[0, 3] == 0)
     check(o, sparse_attn_fp64(q, kv, sink, idx, sc), "masked tiles")
 
 
 def test_tile_largest_count_table(gpu_sa):
-    """kv_len = 32768 needs the 128 KiB count table (dynamic LDS)."""
-    q, kv, sink, idx, sc = rand_case(1, 8, 32768, 64, seed=24)
-    idx[0, :, :32] = torch.arange(32768 - 32, 32768, dtype=torch.int32)  # top rows, shared
+    """kv_len = 16384 needs the 128 KiB count table (dynamic LDS)."""
+    q, kv, sink, idx, sc = rand_case(1, 16, 16384, 64, seed=24)
+    idx[0, :, :32] = torch.arange(16384 - 32, 16384, dtype=torch.int32)  # top rows, shared
     o = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
-    check(o, sparse_attn_fp64(q, kv, sink, idx, sc), "kv_len 32768 tiles")
+    check(o, sparse_attn_fp64(q, kv, sink, idx, sc), "kv_len 16384 tiles")
 
 
 def test_tile_out_of_range_reported(gpu_sa):
@@ -129,7 +147,7 @@ def test_tile_out_of_range_reported(gpu_sa):
 
 
 def test_tile_sink_visible_and_exact_rows(gpu_sa):
-    """q = 0, sink = -inf and a 4-query tile sharing rows: every query's output
+    """q = 0, sink = -inf and a tile whose queries share rows: every query's output
     is exactly the mean of its rows when the rows are duplicates of one row."""
     _, kv, _, _, sc = rand_case(1, 1, 64, 1, seed=26)
     q = torch.zeros(1, 4, 16, 512, dtype=torch.bfloat16)

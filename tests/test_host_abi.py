@@ -181,9 +181,10 @@ def plan_full(host, a, cus):
     (1, 1024, 131072, 2048, 0, False),   # long context: count table too big
     (32, 1, 32768, 2048, 0, False),      # decode: one query per batch, split
     (1, 4096, 4096, 2048, 1, False),     # SA_FLAG_PER_QUERY
-    (1, 8, 32768, 64, 2, True),          # largest count table, no split
-    (1, 8, 32769, 64, 2, False),
-    (1, 3, 100, 64, 2, False),           # fewer queries than a tile
+    (1, 8, 16384, 64, 2, True),          # largest count table, no split
+    (1, 8, 16385, 64, 2, False),
+    (1, 4, 100, 64, 2, True),            # half a tile
+    (1, 3, 100, 64, 2, False),           # fewer queries than half a tile
     (1, 300, 100, 0, 0, False),          # no slots
 ])
 def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
@@ -194,9 +195,10 @@ def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
     assert bool(p["tiles"]) == tiles
     if tiles:
         assert p["nsplit"] == 1
-        assert p["tiles_per_b"] == -(-m // 4) and p["ntiles"] == b * p["tiles_per_b"]
-        assert p["tile_cap"] % 64 == 0 and p["tile_cap"] >= min(kv_len, 4 * topk)
-        assert p["ws"] >= p["ntiles"] * (16 + 8 * p["tile_cap"])
+        assert p["tiles_per_b"] == -(-m // 8) and p["ntiles"] == b * p["tiles_per_b"]
+        assert p["tile_cap"] % 64 == 0 and p["tile_cap"] >= min(kv_len, 8 * topk)
+        # per tile: meta, int32 rows and one count byte per (query, union row)
+        assert p["ws"] >= p["ntiles"] * (16 + (4 + 8) * p["tile_cap"])
 
 
 @pytest.mark.parametrize("b,m,topk,cus,expect_ns,expect_len", [
