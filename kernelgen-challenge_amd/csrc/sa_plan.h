@@ -31,8 +31,10 @@ constexpr int kMetaInts = 4;  // per tile: union size, mode, valid slots, spare
 //    `nsplit` contiguous parts of `split_len` slots, one work-group per part,
 //    merged by the combine kernel when nsplit > 1;
 //  * shared-row path (`tiles`): an index kernel builds each tile's row union,
-//    then tiles whose queries overlap enough run in the shared-row kernel and
-//    the rest in the per-query kernel.
+//    a one-work-group pass orders the tiles by descending step count (longest
+//    first, so the last work-groups to start are the short ones), then tiles
+//    whose queries overlap enough run in the shared-row kernel and the rest in
+//    the per-query kernel.
 struct Plan {
   int64_t units;       // b * m
   int nsplit;          // parts per query (1 = no combine pass)
@@ -42,7 +44,7 @@ struct Plan {
   int64_t ntiles;      // b * tiles_per_b
   int64_t tile_cap;    // union entries stored per tile (multiple of kTileRows);
                        // each has an int32 row and kTileQueries count bytes
-  size_t meta_off, rows_off, cnts_off, part_off;  // workspace byte offsets
+  size_t meta_off, order_off, rows_off, cnts_off, part_off;  // workspace byte offsets
   size_t ws_bytes;     // total workspace
 };
 
@@ -131,6 +133,8 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     p.tile_cap = int64_t(round_up(size_t(cap), kTileRows));
     p.meta_off = off;
     off = round_up(off + size_t(p.ntiles) * kMetaInts * 4, 256);
+    p.order_off = off;
+    off = round_up(off + size_t(p.ntiles) * 4, 256);
     p.rows_off = off;
     off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
     p.cnts_off = off;

@@ -129,6 +129,7 @@ struct TileParams {
   __bf16* o;
   const int32_t* meta;
   int32_t* meta_out;    // same array: a tile that must rescale marks itself per-query
+  const int32_t* order; // work-group i runs tile order[i]
   const int32_t* rows;
   const uint8_t* cnts;
   int64_t m, cap, tiles_per_b;
@@ -451,9 +452,14 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdPara
 // ============================================================================
 // tile index kernel
 // ============================================================================
+// Builds, for one tile of kTQ consecutive queries, the ascending union of the
+// rows its valid slots name and each row's multiplicity in every query.
 // Count layout of a tile: for step s (64 union entries) and tile query q, the
 // 64 count bytes of the step's rows are contiguous at ((s * kTQ) + q) * 64, so
 // a lane reads the counts of 4 consecutive rows of its query as one dword.
+constexpr int kIdxBatch = 8;                       // index loads per thread per batch
+constexpr int kIdxBatchSlots = kIdxBatch * kThreads;
+
 __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexParams p) {
   extern __shared__ unsigned long long s_count[];  // [kv_len], byte q = count in query q
   __shared__ int s_wtot[kWaves];
@@ -478,59 +484,78 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
   if (tid == 0) s_first = kvl;
   __syncthreads();
 
-  bool bad = false;
-  for (int qq = 0; qq < qt; ++qq) {
-    const int32_t* irow = p.idx + bi * p.si_b + (q0 + qq) * p.si_m;
-    int nv = 0;
-    for (int64_t t = tid; t < p.topk; t += kThreads) {
-      const int v = irow[t];
-      if (v >= 0 && v < kvl) {
-        atomicAdd(&s_count[v], 1ull << (8 * qq));
-        ++nv;
-      } else if (v != -1) {
-        bad = true;
-      }
+  // ---- multiplicity table. The slots are read in batches of kIdxBatchSlots
+  // of one query; the next batch's loads are in flight while this one is
+  // counted, so a tile costs about one memory latency per batch.
+  const int64_t nbq = (p.topk + kIdxBatchSlots - 1) / kIdxBatchSlots;  // batches per query
+  const int64_t nbt = nbq * qt;
+  const int32_t* ib = p.idx + bi * p.si_b + q0 * p.si_m;
+  auto load = [&](int64_t k, int (&v)[kIdxBatch]) {
+    const int64_t qq = k / nbq;
+    const int64_t t0 = (k - qq * nbq) * kIdxBatchSlots + tid;
+    const int32_t* irow = ib + qq * p.si_m;
+#pragma unroll
+    for (int u = 0; u < kIdxBatch; ++u) {
+      const int64_t t = t0 + u * kThreads;
+      v[u] = t < p.topk ? irow[t] : -1;  // past the end: skipped like a -1 slot
     }
-    for (int off = 32; off > 0; off >>= 1) nv += __shfl_xor(nv, off);
-    if (lane == 0) atomicAdd(&s_nv[qq], nv);
+  };
+  bool bad = false;
+  int va[kIdxBatch], vb[kIdxBatch];
+#pragma unroll
+  for (int u = 0; u < kIdxBatch; ++u) va[u] = vb[u] = -1;
+  if (nbt > 0) load(0, va);
+  for (int64_t k = 0; k < nbt; ++k) {
+    if (k + 1 < nbt) load(k + 1, vb);
+    const int qq = int(k / nbq);
+    const unsigned long long one = 1ull << (8 * qq);
+    int nv = 0;  // wave-uniform
+#pragma unroll
+    for (int u = 0; u < kIdxBatch; ++u) {
+      const int v = va[u];
+      const bool ok = v >= 0 && v < kvl;
+      if (ok) atomicAdd(&s_count[v], one);
+      bad |= !ok && v != -1;
+      nv += __popcll(__ballot(ok));
+    }
+    if (lane == 0 && nv != 0) atomicAdd(&s_nv[qq], nv);
+#pragma unroll
+    for (int u = 0; u < kIdxBatch; ++u) va[u] = vb[u];
   }
   if (bad && p.err != nullptr) atomicOr(p.err, 1);
   __syncthreads();
 
-  // contiguous chunk per thread keeps the union in ascending row order
-  const int chunk = (kvl + kThreads - 1) / kThreads;
-  const int lo = min(kvl, tid * chunk);
-  const int hi = min(kvl, lo + chunk);
-  int c = 0;
+  // ---- ascending union. Wave w scans a contiguous run of 64-row chunks; a
+  // ballot per chunk ranks its nonzero rows, so each wave writes its part of
+  // the union with consecutive lanes on consecutive entries.
+  const int nchunks = (kvl + 63) / 64;
+  const int cpw = (nchunks + kWaves - 1) / kWaves;
+  const int c_lo = min(nchunks, wave * cpw);
+  const int c_hi = min(nchunks, c_lo + cpw);
+  int wcount = 0;  // wave-uniform
+  int wfirst = kvl;
   int bsum[kTQ];
 #pragma unroll
   for (int k = 0; k < kTQ; ++k) bsum[k] = 0;
-  int first = kvl;
-  for (int i = lo; i < hi; ++i) {
-    const unsigned long long w = s_count[i];
-    if (w != 0ull) {
-      if (c == 0) first = i;
-      ++c;
+  for (int c = c_lo; c < c_hi; ++c) {
+    const int i = c * 64 + lane;
+    const unsigned long long w = i < kvl ? s_count[i] : 0ull;
+    const unsigned long long bm = __ballot(w != 0ull);
+    if (bm != 0ull && wfirst == kvl) wfirst = c * 64 + __ffsll((long long)bm) - 1;
+    wcount += __popcll(bm);
 #pragma unroll
-      for (int k = 0; k < kTQ; ++k) bsum[k] += int((w >> (8 * k)) & 255ull);
-    }
+    for (int k = 0; k < kTQ; ++k) bsum[k] += int((w >> (8 * k)) & 255ull);
   }
-  int incl = c;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off);
-    if (lane >= off) incl += t;
-  }
-  if (lane == 63) s_wtot[wave] = incl;
+  if (lane == 0) s_wtot[wave] = wcount;
 #pragma unroll
   for (int k = 0; k < kTQ; ++k) {
     int v = bsum[k];
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    if (lane == 0) atomicAdd(&s_bsum[k], v);
+    if (lane == 0 && v != 0) atomicAdd(&s_bsum[k], v);
   }
-  if (c > 0) atomicMin(&s_first, first);
+  if (lane == 0 && wfirst < kvl) atomicMin(&s_first, wfirst);
   __syncthreads();
-  int pos = incl - c;
+  int pos = 0;
   int nU = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -546,9 +571,13 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
 #pragma unroll
     for (int k = 0; k < kTQ; ++k) cb[k * kTileRows] = uint8_t((w >> (8 * k)) & 255ull);
   };
-  for (int i = lo; i < hi; ++i) {
-    const unsigned long long w = s_count[i];
-    if (w != 0ull) put(pos++, i, w);
+  const unsigned long long below = (1ull << lane) - 1ull;  // lanes under this one
+  for (int c = c_lo; c < c_hi; ++c) {
+    const int i = c * 64 + lane;
+    const unsigned long long w = i < kvl ? s_count[i] : 0ull;
+    const unsigned long long bm = __ballot(w != 0ull);
+    if (w != 0ull) put(pos + __popcll(bm & below), i, w);
+    pos += __popcll(bm);
   }
   // pad to whole 64-row steps with a valid row of count 0
   const int padded = (nU + kTileRows - 1) / kTileRows * kTileRows;
@@ -573,13 +602,60 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
 }
 
 // ============================================================================
+// tile order kernel
+// ============================================================================
+// One work-group sorts the tiles by descending step count (a counting sort:
+// keys are 0..kMaxTileKv/64, per-query tiles get key 0). The shared-row
+// kernel's work-group i runs tile order[i]; work-groups start in index order,
+// so the longest tiles start first and the short ones fill in at the end.
+// Tiles with equal keys may come in any order: each tile is independent.
+constexpr int kOrderThreads = 1024;
+constexpr int kOrderKeys = int(sa::kMaxTileKv / kTileRows) + 1;
+constexpr int kOrderKeysPadded = (kOrderKeys + 63) / 64 * 64;
+
+__global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const int32_t* meta,
+                                                                      int32_t* order,
+                                                                      int ntiles) {
+  __shared__ int s_pos[kOrderKeysPadded];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kOrderKeysPadded; i += kOrderThreads) s_pos[i] = 0;
+  __syncthreads();
+  auto key = [&](int t) {
+    const int32_t* mt = meta + int64_t(t) * kMetaInts;
+    return mt[1] == kModeShared ? (mt[0] + kTileRows - 1) / kTileRows : 0;
+  };
+  for (int t = tid; t < ntiles; t += kOrderThreads) atomicAdd(&s_pos[key(t)], 1);
+  __syncthreads();
+  if (tid < 64) {
+    // exclusive scan over descending keys: the start of key k is the number
+    // of tiles with a larger key
+    int carry = 0;
+    for (int c = kOrderKeysPadded / 64 - 1; c >= 0; --c) {
+      const int k = 64 * c + 63 - tid;  // lane 0 takes the largest key of the chunk
+      const int v = s_pos[k];
+      int incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (tid >= off) incl += t;
+      }
+      s_pos[k] = carry + incl - v;
+      carry += __shfl(incl, 63);
+    }
+  }
+  __syncthreads();
+  for (int t = tid; t < ntiles; t += kOrderThreads) order[atomicAdd(&s_pos[key(t)], 1)] = t;
+}
+
+// ============================================================================
 // shared-row tile kernel
 // ============================================================================
-// LDS row layout: a gathered row is 1 KiB stored at a 1040-byte pitch. The
-// 16-byte shift per row spreads the ds_read_b128 K reads of 16 consecutive
-// rows over all 64 banks, and every K/V read of a lane is its base address
-// plus a compile-time offset.
-constexpr int kTilePitch = kRowBytes + 16;
+// LDS row layout: a gathered row is 1 KiB stored at a 1056-byte pitch, and
+// every K/V read of a lane is its base address plus a compile-time offset.
+// Measured on gfx950 with 4 waves per CU, for this kernel's read patterns:
+// ds_read_b64_tr_b16 (V) reaches 116 B/clk at this pitch against 91 at
+// 1040, 1072 or 1088 and 63 at 1024; ds_read_b128 (K) 120 B/clk (125 at 1040).
+constexpr int kTilePitch = kRowBytes + 32;
 
 // Each wave owns two queries of the tile outright: their Q^T (128 VGPRs),
 // their O[32 columns x 512 d] (16 blocks of 32 x 32 fp32, in AGPRs), their
@@ -605,7 +681,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  const int64_t tile = blockIdx.x;
+  const int64_t tile = p.order[blockIdx.x];
   const int32_t* meta = p.meta + tile * kMetaInts;
   if (meta[1] != kModeShared) return;
   const int nU = meta[0];
@@ -1016,6 +1092,10 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), lds,
                        stream, ip);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
+    int32_t* order = reinterpret_cast<int32_t*>(ws + plan.order_off);
+    hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream,
+                       static_cast<const int32_t*>(ip.meta), order, int(plan.ntiles));
+    if (hipGetLastError() != hipSuccess) return SA_EHIP;
 
     TileParams tp{};
     tp.q = p.q;
@@ -1024,6 +1104,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     tp.o = p.o;
     tp.meta = ip.meta;
     tp.meta_out = ip.meta;
+    tp.order = order;
     tp.rows = ip.rows;
     tp.cnts = ip.cnts;
     tp.m = a->m;
