@@ -34,9 +34,15 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are kept out of every gfx950 code object.
+# -amdgpu-mfma-vgpr-form: compiler-generated MFMAs accumulate in VGPRs. The
+# shared-row kernel issues its O += P . V MFMAs as inline assembly with AGPR
+# accumulators (all 256 AGPRs hold O) and its S = K . Q^T MFMAs through the
+# compiler; without the flag the compiler also gives S AGPRs and shuffles
+# part of O through VGPRs every step.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-shared",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

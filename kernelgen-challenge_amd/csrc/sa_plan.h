@@ -122,9 +122,12 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     p.nsplit = 1;
     p.split_len = a->topk;
   }
+  // the shared-row kernel addresses rows by 32-bit byte offsets in the batch
+  const bool offsets32 =
+      a->kv_len > 0 && (a->kv_len - 1) * a->skv[1] * 2 + 2 * kDim <= int64_t(UINT32_MAX);
   p.tiles = p.nsplit == 1 && (a->flags & SA_FLAG_PER_QUERY) == 0 &&
             a->m >= kTileQueries / 2 && a->topk > 0 && a->kv_len > 0 &&
-            a->kv_len <= kMaxTileKv;
+            a->kv_len <= kMaxTileKv && offsets32;
   size_t off = 0;
   if (p.tiles) {
     p.tiles_per_b = (a->m + kTileQueries - 1) / kTileQueries;

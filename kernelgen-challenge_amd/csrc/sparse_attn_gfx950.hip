@@ -114,10 +114,11 @@ struct IndexParams {
   const int32_t* idx;
   int32_t* err;
   int32_t* meta;        // [ntiles][kMetaInts]
-  int32_t* rows;        // [ntiles][cap]
+  uint32_t* row_off;    // [ntiles][cap] byte offsets of the union rows in the batch's kv
   uint8_t* cnts;        // [ntiles][cap / 64][kTQ][64] multiplicity bytes
   int64_t m, kv_len, topk;
   int64_t si_b, si_m;
+  int64_t skv_n;        // kv row stride (elements)
   int64_t tiles_per_b, cap;
   int force;            // shared mode whenever the counts fit
 };
@@ -130,7 +131,7 @@ struct TileParams {
   const int32_t* meta;
   int32_t* meta_out;    // same array: a tile that must rescale marks itself per-query
   const int32_t* order; // work-group i runs tile order[i]
-  const int32_t* rows;
+  const uint32_t* row_off;
   const uint8_t* cnts;
   int64_t m, cap, tiles_per_b;
   int64_t sq_b, sq_m, sq_h;
@@ -160,6 +161,33 @@ __device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// Four v_mfma_f32_32x32x16_bf16 sharing one B operand, accumulating in AGPRs.
+// Issued as inline assembly so that the compiler's own MFMAs in the same
+// kernel keep their accumulators in VGPRs (the library is built with
+// -amdgpu-mfma-vgpr-form): the shared-row kernel needs all 256 AGPRs for O
+// and 32 VGPRs for S at the same time. Hazards the compiler cannot see:
+//  * a VALU write of an A/B operand register needs 2 wait states before the
+//    MFMA reads it: s_nop 2 gives 3;
+//  * back-to-back accumulation into the same registers needs none;
+//  * AGPR reads of the results (v_accvgpr_read) need the MFMA's 8 passes plus
+//    3: mfma_agpr_drain() gives 16 wait states.
+__device__ __forceinline__ void mfma4_agpr(f32x16& c0, f32x16& c1, f32x16& c2, f32x16& c3,
+                                           bf16x8 a0, bf16x8 a1, bf16x8 a2, bf16x8 a3,
+                                           bf16x8 b) {
+  asm volatile(
+      "s_nop 2\n\t"
+      "v_mfma_f32_32x32x16_bf16 %0, %4, %8, %0\n\t"
+      "v_mfma_f32_32x32x16_bf16 %1, %5, %8, %1\n\t"
+      "v_mfma_f32_32x32x16_bf16 %2, %6, %8, %2\n\t"
+      "v_mfma_f32_32x32x16_bf16 %3, %7, %8, %3"
+      : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(b));
+}
+
+__device__ __forceinline__ void mfma_agpr_drain() {
+  asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the address
 // of 4 consecutive bf16 (row j/4, columns 4*(j%4)..+3 of a 4 x 16 block) and
 // receives column j of that block (4 values, one per row).
@@ -187,6 +215,20 @@ __device__ __forceinline__ void lds_dma16_async(const void* gsrc, void* lds) {
       "global_load_lds_dwordx4 %0, off"
       :
       : "v"(gsrc), "s"(lds_addr)
+      : "memory", "m0");
+}
+
+// LDS-DMA of one 1 KiB row at a wave-uniform address: SGPR base `row` plus the
+// 32-bit lane offset 16 * lane, into LDS bytes lds_addr + 16 * lane. Measured
+// on gfx950, this form blocks the issuing wave for about 27 cycles against 46
+// for the same transfer with a 64-bit per-lane address.
+__device__ __forceinline__ void lds_dma_row(const void* row, uint32_t lane_off, uint32_t lds_addr) {
+  asm volatile(
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(lane_off), "s"(row), "s"(lds_addr)
       : "memory", "m0");
 }
 
@@ -563,10 +605,11 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
     pos += (w < wave) ? t : 0;
     nU += t;
   }
-  int32_t* rows = p.rows + tile * p.cap;
+  uint32_t* row_off = p.row_off + tile * p.cap;
   uint8_t* cnts = p.cnts + tile * p.cap * kTQ;
+  const uint32_t row_bytes = uint32_t(p.skv_n) * 2u;  // the plan keeps offsets in 32 bits
   auto put = [&](int e, int row, unsigned long long w) {
-    rows[e] = row;
+    row_off[e] = uint32_t(row) * row_bytes;
     uint8_t* cb = cnts + (e / kTileRows) * (kTQ * kTileRows) + (e % kTileRows);
 #pragma unroll
     for (int k = 0; k < kTQ; ++k) cb[k * kTileRows] = uint8_t((w >> (8 * k)) & 255ull);
@@ -650,28 +693,33 @@ __global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const int3
 // ============================================================================
 // shared-row tile kernel
 // ============================================================================
-// LDS row layout: a gathered row is 1 KiB stored at a 1056-byte pitch, and
+// LDS row layout: a gathered row is 1 KiB stored at a 1072-byte pitch, and
 // every K/V read of a lane is its base address plus a compile-time offset.
-// Measured on gfx950 with 4 waves per CU, for this kernel's read patterns:
-// ds_read_b64_tr_b16 (V) reaches 116 B/clk at this pitch against 91 at
-// 1040, 1072 or 1088 and 63 at 1024; ds_read_b128 (K) 120 B/clk (125 at 1040).
-constexpr int kTilePitch = kRowBytes + 32;
+// Measured on gfx950 (4 waves per CU, 8 reads in flight per wave), for this
+// kernel's read patterns: ds_read_b128 of K reaches 248 B/clk per CU at 1040,
+// 1072 or 1104 and 128 at 1056; the transposing ds_read_b64_tr_b16 of V
+// reaches 253 B/clk at 1056, 1072 or 1104 and 128 at 1040.
+constexpr int kTilePitch = kRowBytes + 48;
 
-// Each wave owns two queries of the tile outright: their Q^T (128 VGPRs),
-// their O[32 columns x 512 d] (16 blocks of 32 x 32 fp32, in AGPRs), their
-// softmax state and P. The four waves share only the gathered rows, so the
-// one barrier per step is the gather's.
-//   S^T block rb (rows 32rb..32rb+31 of the step) x the wave's 32 columns:
-//     lane (l32, hi) holds column l32 (query 2w + l32/16, head l32 % 16) and
-//     rows 32rb + 8a + 4hi + b in register 4a + b.
-//   PV k-block kb (16 rows) takes k-group hi = rows 16kb + 4hi + (0..3) and
-//     16kb + 8 + 4hi + (0..3): exactly this lane's S^T registers, so P feeds
-//     the MFMA A operand without leaving registers.
-//   O block nb: column n < 16 is d = 128(nb/4) + 16(nb%4) + n, column n >= 16
-//     is d = 128(nb/4) + 64 + 16(nb%4) + n - 16; rows are the 32 (query, head)
-//     columns in the S^T register order.
+// Work split of a tile step (64 union rows x 8 queries x 16 heads):
+//  * S^T = K . Q^T and the softmax: wave w owns two queries (32 score
+//    columns): their Q^T (128 VGPRs), softmax state and sums.
+//      S^T block rb (rows 32rb..32rb+31) x the wave's 32 columns: lane
+//      (l32, hi) holds column l32 (query 2w + l32/16, head l32 % 16) and rows
+//      32rb + 8a + 4hi + b in register 4a + b.
+//  * P goes to LDS as bf16 P[column][row] (one 144-byte line per column).
+//  * O = P . V: wave w owns d = 128w..128w+127 of all 128 columns (16 blocks
+//    of 32 x 32 fp32 in AGPRs). Each wave reads P (16 KiB) and its quarter of
+//    V (16 KiB) per step instead of all of V (64 KiB).
+//      block (cb, db): rows are columns 32cb + 8(i/4) + 4hi + i%4 (register
+//      i), MFMA column l32 is d = 128w + 32db + l32.
+// Barriers per step: one after P is written (LDS only) and the gather's.
+constexpr int kPPitch = 2 * kTileRows + 16;  // bytes per P column line
+constexpr int kTileCols = kTQ * kHeads;      // 128 score columns
+
 __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kTilePitch];
+  __shared__ __attribute__((aligned(16))) uint8_t s_p[kTileCols * kPPitch];
   __shared__ __attribute__((aligned(16))) uint8_t s_cnt[2][kTQ * kTileRows];
   __shared__ int s_abort;
 
@@ -717,20 +765,24 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       for (int e = 0; e < 8; ++e) qf[s][e] = static_cast<__bf16>(0.f);
   }
 
-  const int32_t* urows = p.rows + tile * p.cap;
+  const uint32_t* urows = p.row_off + tile * p.cap;
   const uint8_t* ucnts = p.cnts + tile * p.cap * kTQ;
-  const __bf16* kvb = p.kv + bi * p.skv_b;
+  const uint8_t* kvb = reinterpret_cast<const uint8_t*>(p.kv + bi * p.skv_b);
+  // LDS address of this wave's first tile row in buffer 0
+  const uint32_t lds_rows = __builtin_amdgcn_readfirstlane(uint32_t(
+      reinterpret_cast<uintptr_t>((lds_u8_t*)&s_tile[0][wave * kRowsPerWave * kTilePitch])));
 
-  // Union rows of a step: lane i (< 16) of wave w holds row 16w + i. The
-  // gather reads them back with readlane, so its row addresses are scalar.
+  // Union rows of a step: lane i (< 16) of wave w holds the byte offset of
+  // row 16w + i. The gather reads them back with readlane, so each row's
+  // address is a scalar base.
   auto step_rows = [&](int step) -> int {
-    return urows[step * kTileRows + wave * kRowsPerWave + (lane & 15)];
+    return int(urows[step * kTileRows + wave * kRowsPerWave + (lane & 15)]);
   };
   // One 1 KiB row into LDS row 16w + i (lane l moves bytes 16l..16l+15).
   auto dma_row = [&](int rows_v, int i, int buf) {
-    const int row = __builtin_amdgcn_readlane(rows_v, i);
-    lds_dma16_async(kvb + int64_t(row) * p.skv_n + 8 * lane,
-                    &s_tile[buf][(wave * kRowsPerWave + i) * kTilePitch]);
+    const uint32_t off = uint32_t(__builtin_amdgcn_readlane(rows_v, i));
+    lds_dma_row(kvb + off, 16 * lane,
+                lds_rows + uint32_t(buf * kTileRows * kTilePitch + i * kTilePitch));
   };
   // The 512 count bytes of a step (wave 0, lanes 0..31).
   auto dma_counts = [&](int step, int buf) {
@@ -740,7 +792,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 
   float m_run = -INFINITY;  // reference max of column l32 (log2 domain)
   float l_run = 0.f;        // this lane's share of the column's sum
-  f32x16 oacc[kDim / 32];
+  f32x16 oacc[kDim / 32];   // [cb * 4 + db]
 #pragma unroll
   for (int nb = 0; nb < kDim / 32; ++nb) {
 #pragma unroll
@@ -760,11 +812,55 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 
   // K operand: lane reads row 32rb + l32, bytes 32s + 16hi.
   const int koff = l32 * kTilePitch + 16 * hi;
-  // V operand: 16-lane group G reads rows 16kb + 4(G>>1) + j/4 (and + 8),
-  // bytes 2 * (64(G&1) + 4(j&3)) of each 32-column block.
+  // V operand (B of O = P . V): 16-lane group G, lane j reads row
+  // 16kb + 8(G>>1) + j/4 (and 4 rows on), d = 128w + 32db + 16(G&1) + 4(j&3)
+  // .. +3, and receives d = 128w + 32db + 16(G&1) + j over 4 rows.
   const int G = lane >> 4;
   const int j = lane & 15;
-  const int voff = (4 * (G >> 1) + (j >> 2)) * kTilePitch + 128 * (G & 1) + 8 * (j & 3);
+  const int voff =
+      (8 * (G >> 1) + (j >> 2)) * kTilePitch + 2 * (128 * wave + 16 * (G & 1) + 4 * (j & 3));
+  // P operand (A): lane reads column 32cb + l32, rows 16kb + 8hi .. +7.
+  const uint8_t* pread = s_p + l32 * kPPitch + 16 * hi;
+  // P store: this lane's column 32w + l32, rows 32rb + 8a + 4hi .. +3.
+  uint8_t* pwrite = s_p + (32 * wave + l32) * kPPitch + 8 * hi;
+
+  // Softmax of one 32-row half of a step, cut into slots that ride between
+  // MFMAs: slots 0..7 mask and scale two scores each and take the column max,
+  // slot 8 merges the max of the lane pair and checks / sets the column's
+  // reference, slots 9..24 turn one score each into c * 2^(s - m), add it to
+  // the column sum and store P as bf16 (every fourth slot).
+  constexpr int kSmSlots = 25;
+  bool abort_any = false;  // wave-uniform: a column jumped above its reference
+  auto sm_slot = [&](int k, f32x16& x, const uint32_t(&cw)[4], int rb, float& mx, float& mref,
+                     float& psum, bf16x4& pk) {
+    if (k < 8) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int e = 2 * k + t;
+        const bool valid = ((cw[e >> 2] >> (8 * (e & 3))) & 255u) != 0u;
+        const float sv = valid ? x[e] * p.scale_log2 : -INFINITY;
+        x[e] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    } else if (k == 8) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                       false, false);
+      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // -inf: no row in the half
+      // Fixed reference: a column keeps the max of its first non-empty half.
+      // A later score more than kTileMaxJump above it would need O rescaled;
+      // the tile then hands itself to the per-query kernel.
+      abort_any |= __any(m_run != -INFINITY && mx > m_run + kTileMaxJump) != 0;
+      if (m_run == -INFINITY) m_run = mx;
+      mref = m_run == -INFINITY ? 0.f : m_run;  // column still empty
+    } else if (k < kSmSlots) {
+      const int e = k - 9;
+      const float cnt = float((cw[e >> 2] >> (8 * (e & 3))) & 255u);
+      const float pj = cnt * __builtin_amdgcn_exp2f(x[e] - mref);  // 0 for masked rows
+      psum += pj;
+      pk[e & 3] = static_cast<__bf16>(pj);
+      if ((e & 3) == 3) *reinterpret_cast<bf16x4*>(pwrite + 2 * (32 * rb + 8 * (e >> 2))) = pk;
+    }
+  };
 
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
@@ -772,139 +868,115 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     const uint8_t* cb = s_cnt[buf];
     const int nxt = min(step + 1, nsteps - 1);  // the last step refetches itself: harmless
 
-    // ---- S^T = K . Q^T for both row blocks; next step's rows 0..7 gathered ----
-    // One k-step (2 MFMAs) per group; K fragments are read two groups ahead
-    // into a 3-slot register ring so LDS latency hides behind the MFMAs.
-    f32x16 sacc[2];
+    // counts of this lane's rows in its query: rows 32rb + 8a + 4hi + (0..3)
+    uint32_t cw0[4], cw1[4];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int a = 0; a < 4; ++a) {
+      cw0[a] = *reinterpret_cast<const uint32_t*>(&cb[qw * kTileRows + 8 * a + 4 * hi]);
+      cw1[a] = *reinterpret_cast<const uint32_t*>(&cb[qw * kTileRows + 32 + 8 * a + 4 * hi]);
+    }
+
+    // ---- S^T = K . Q^T, rows 0..31 then 32..63; the softmax of rows 0..31 runs
+    // between the MFMAs of rows 32..63. All 16 rows of this wave's share of the
+    // next step are gathered here, so they have the rest of the step to land.
+    f32x16 sacc0, sacc1;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[rb][i] = 0.f;
+    for (int i = 0; i < 16; ++i) {
+      sacc0[i] = 0.f;
+      sacc1[i] = 0.f;
+    }
     {
-      const uint8_t* kr0 = tb + koff;
-      const uint8_t* kr1 = kr0 + 32 * kTilePitch;
-      bf16x8 kf[3][2];
-      auto kread = [&](int s, int slot) {
-        kf[slot][0] = *reinterpret_cast<const bf16x8*>(kr0 + 32 * s);
-        kf[slot][1] = *reinterpret_cast<const bf16x8*>(kr1 + 32 * s);
+      const uint8_t* kr = tb + koff;
+      bf16x8 kf[3];
+      auto kread = [&](int i, int slot) {
+        kf[slot] = *reinterpret_cast<const bf16x8*>(kr + (i >> 5) * 32 * kTilePitch + 32 * (i & 31));
       };
       kread(0, 0);
       kread(1, 1);
+      float mx = -INFINITY, mref = 0.f, psum = 0.f;
+      bf16x4 pk;
 #pragma unroll
-      for (int s = 0; s < kDim / 16; ++s) {
-        if (s + 2 < kDim / 16) kread(s + 2, (s + 2) % 3);
-        sacc[0] = mfma_32x32x16(kf[s % 3][0], qf[s], sacc[0]);
-        sacc[1] = mfma_32x32x16(kf[s % 3][1], qf[s], sacc[1]);
-        if ((s & 3) == 3) dma_row(rows_next, s >> 2, buf ^ 1);
-        __builtin_amdgcn_sched_barrier(0);  // keep the read-ahead order
+      for (int i = 0; i < 2 * (kDim / 16); ++i) {
+        if (i + 2 < 2 * (kDim / 16)) kread(i + 2, (i + 2) % 3);
+        if (i < kDim / 16)
+          sacc0 = mfma_32x32x16(kf[i % 3], qf[i], sacc0);
+        else
+          sacc1 = mfma_32x32x16(kf[i % 3], qf[i - kDim / 16], sacc1);
+        if ((i & 3) == 3) dma_row(rows_next, i >> 2, buf ^ 1);
+        if (i == 1) dma_counts(nxt, buf ^ 1);
+        if (i >= kDim / 16) sm_slot(i - kDim / 16, sacc0, cw0, 0, mx, mref, psum, pk);
+        __builtin_amdgcn_sched_barrier(0);  // keep the interleave
       }
+      l_run += psum;
     }
-    // S^T goes to VALU next: keep it in VGPRs (AGPRs hold O)
-    asm volatile("" : "+v"(sacc[0]), "+v"(sacc[1]));
+    rows_next = step_rows(min(step + 2, nsteps - 1));
+    lds_barrier();  // P rows 0..31 of every column are in LDS
 
-    // counts of this lane's rows in its query: rows 32rb + 8a + 4hi + (0..3)
-    uint32_t cw[2][4];
+    // ---- O += P . V over 32 rows (k-blocks kb0, kb0 + 1): per k-block 4 P
+    // fragments (b128, the second k-block's read during the first) and 4 V
+    // fragments (2 transposing reads each) read two ahead into a 3-slot ring;
+    // each V fragment feeds 4 MFMAs. `extra(n)` is VALU work placed before the
+    // n-th group of 4 MFMAs.
+    auto pv_half = [&](int kb0, auto&& extra) {
+      bf16x8 af[2][4];
+      bf16x8 vf[3];
+      auto pread_kb = [&](int kb, int slot) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-        cw[rb][a] = *reinterpret_cast<const uint32_t*>(
-            &cb[qw * kTileRows + 32 * rb + 8 * a + 4 * hi]);
-
-    // ---- masking, column max over the step's 64 rows, lazy rescale ---------------
-    float mx = -INFINITY;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int a = 0; a < 4; ++a)
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const bool valid = ((cw[rb][a] >> (8 * b)) & 255u) != 0u;
-          const float s = valid ? sacc[rb][4 * a + b] * p.scale_log2 : -INFINITY;
-          sacc[rb][4 * a + b] = s;
-          mx = fmaxf(mx, s);
-        }
-    {
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                       false, false);
-      mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // -inf: no row this step
-    }
-    // Fixed reference: a column keeps the max of its first non-empty step. A
-    // later step more than kTileMaxJump above it would need O rescaled; the
-    // tile then hands itself to the per-query kernel (which rescales online).
-    if (__any(m_run != -INFINITY && mx > m_run + kTileMaxJump)) s_abort = 1;
-    if (m_run == -INFINITY) m_run = mx;
-    const float mref = m_run == -INFINITY ? 0.f : m_run;  // column still empty
-    float psum = 0.f;
-
-    // ---- O += P . V over 4 k-blocks of 16 rows; next step's rows 8..15 gathered ----
-    // P of k-block kb (bf16 A operand) straight from this lane's S^T registers.
-    auto make_pa = [&](int kb) -> bf16x8 {
-      const int rb = kb >> 1;
-      const int a0 = 2 * (kb & 1);
-      bf16x8 pa;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int a = a0 + (e >> 2);
-        const int b = e & 3;
-        const float cnt = float((cw[rb][a] >> (8 * b)) & 255u);
-        const float pj = cnt * exp2f(sacc[rb][4 * a + b] - mref);  // c * 2^(s - m)
-        psum += pj;
-        pa[e] = static_cast<__bf16>(pj);
-      }
-      return pa;
-    };
-    // Groups of 2 d-blocks (2 MFMAs, 4 transposing reads); V fragments are
-    // read two groups ahead into a 3-slot register ring.
-    {
-      constexpr int kGroups = (kTileRows / 16) * (kDim / 64);  // 4 k-blocks x 8 groups
-      bf16x4 vv[3][4];
-      auto vread = [&](int g, int slot) {
-        const int kb = g >> 3;
-        const uint8_t* v0p = tb + voff + 16 * kb * kTilePitch;
-        const uint8_t* v1p = v0p + 8 * kTilePitch;
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int nb = 2 * (g & 7) + i;
-          const int cb2 = 256 * (nb >> 2) + 32 * (nb & 3);  // bytes of d = 128(nb/4) + 16(nb%4)
-          vv[slot][2 * i] = lds_read_tr16(v0p + cb2);
-          vv[slot][2 * i + 1] = lds_read_tr16(v1p + cb2);
-        }
+        for (int c = 0; c < 4; ++c)
+          af[slot][c] = *reinterpret_cast<const bf16x8*>(pread + c * 32 * kPPitch + 32 * kb);
       };
-      bf16x8 pa = make_pa(0);
-      bf16x8 pa_next = pa;
+      auto vread = [&](int n, int slot) {
+        const uint8_t* v0 = tb + voff + 16 * (kb0 + (n >> 2)) * kTilePitch + 64 * (n & 3);
+        const bf16x4 lo = lds_read_tr16(v0);
+        const bf16x4 up = lds_read_tr16(v0 + 4 * kTilePitch);
+        vf[slot] = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
+      };
+      pread_kb(kb0, 0);
       vread(0, 0);
       vread(1, 1);
 #pragma unroll
-      for (int g = 0; g < kGroups; ++g) {
-        const int kb = g >> 3;
-        if (g + 2 < kGroups) vread(g + 2, (g + 2) % 3);
-        if ((g & 7) == 0 && kb + 1 < kTileRows / 16) pa_next = make_pa(kb + 1);
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const bf16x4 v0 = vv[g % 3][2 * i];
-          const bf16x4 v1 = vv[g % 3][2 * i + 1];
-          const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-          const int nb = 2 * (g & 7) + i;
-          oacc[nb] = mfma_32x32x16(pa, vf, oacc[nb]);
-        }
-        if ((g & 3) == 3) dma_row(rows_next, 8 + (g >> 2), buf ^ 1);
-        if ((g & 7) == 7) pa = pa_next;
+      for (int n = 0; n < 8; ++n) {
+        const int kb = n >> 2;
+        const int db = n & 3;
+        if (n + 2 < 8) vread(n + 2, (n + 2) % 3);
+        if (n == 0) pread_kb(kb0 + 1, 1);
+        extra(n);
+        mfma4_agpr(oacc[db], oacc[4 + db], oacc[8 + db], oacc[12 + db], af[kb][0], af[kb][1],
+                   af[kb][2], af[kb][3], vf[n % 3]);
         __builtin_amdgcn_sched_barrier(0);  // keep the read-ahead order
       }
+    };
+
+    // ---- O += P . V, rows 0..31, with the softmax of rows 32..63 -----------------
+    {
+      float mx = -INFINITY, mref = 0.f, psum = 0.f;
+      bf16x4 pk;
+      pv_half(0, [&](int n) {
+#pragma unroll
+        for (int k = (kSmSlots * n + 7) / 8; k < (kSmSlots * (n + 1) + 7) / 8; ++k)
+          sm_slot(k, sacc1, cw1, 1, mx, mref, psum, pk);
+      });
+      l_run += psum;
     }
-    l_run += psum;
-    dma_counts(nxt, buf ^ 1);
-    rows_next = step_rows(min(step + 2, nsteps - 1));
-    dma_barrier();  // every wave's prefetch has landed
-    if (s_abort != 0) {  // uniform: read after the barrier by every wave
+    if (abort_any) s_abort = 1;
+    lds_barrier();  // P rows 32..63 are in LDS; every abort of this step is set
+    const int abort_seen = s_abort;
+
+    // ---- O += P . V, rows 32..63 -------------------------------------------------
+    pv_half(2, [](int) {});
+
+    dma_barrier();  // every wave's prefetch has landed; P and this tile are free
+    if (abort_seen != 0) {  // uniform: every wave read it after the same barrier
       if (tid == 0) p.meta_out[tile * kMetaInts + 1] = sa::kModePerQuery;
-      return;            // no o written; no transfer in flight
+      return;               // no o written; no transfer in flight
     }
   }
 
   // ---- epilogue: column sums, sink fold, bf16 store -----------------------------
-  float f;
+  mfma_agpr_drain();
+  // The owner lane of a column computes its normalizer; P's LDS lines are free
+  // after the last barrier and carry the 128 normalizers to every wave.
+  float* s_f = reinterpret_cast<float*>(s_p);
   {
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run),
                                                      __float_as_uint(l_run), false, false);
@@ -912,21 +984,25 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     const float sink2 = p.sink[hh] * kLog2e;
     const float mt = fmaxf(m_run, sink2);
     const float a = exp2f(m_run - mt);  // 0 when the column has no valid slot
-    f = a / (a * lt + exp2f(sink2 - mt));
+    if (hi == 0) s_f[32 * wave + l32] = a / (a * lt + exp2f(sink2 - mt));
   }
-  __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + (l32 & 15) + 64 * (l32 >> 4);
+  lds_barrier();
+  __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + 128 * wave + l32;
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int c = 0; c < 4; ++c)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int cidx = 8 * a + 4 * hi + b;  // O row = S^T column of the wave
-      const float fs = __shfl(f, cidx);
-      const int q2 = 2 * wave + (cidx >> 4);
+    for (int a = 0; a < 4; ++a) {
+      const int col0 = 32 * c + 8 * a + 4 * hi;  // columns col0 .. col0 + 3
+      const f32x4 fs = *reinterpret_cast<const f32x4*>(&s_f[col0]);
+      const int q2 = col0 >> 4;
       if (q2 < qt) {
-        __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t(cidx & 15) * p.so_h;
 #pragma unroll
-        for (int nb = 0; nb < kDim / 32; ++nb)
-          orow[128 * (nb >> 2) + 16 * (nb & 3)] = static_cast<__bf16>(oacc[nb][4 * a + b] * fs);
+        for (int b = 0; b < 4; ++b) {
+          __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t((col0 + b) & 15) * p.so_h;
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+            orow[32 * db] = static_cast<__bf16>(oacc[4 * c + db][4 * a + b] * fs[b]);
+        }
       }
     }
 }
@@ -1074,13 +1150,14 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     ip.idx = a->idx;
     ip.err = a->err_word;
     ip.meta = reinterpret_cast<int32_t*>(ws + plan.meta_off);
-    ip.rows = reinterpret_cast<int32_t*>(ws + plan.rows_off);
+    ip.row_off = reinterpret_cast<uint32_t*>(ws + plan.rows_off);
     ip.cnts = ws + plan.cnts_off;
     ip.m = a->m;
     ip.kv_len = a->kv_len;
     ip.topk = a->topk;
     ip.si_b = a->sidx[0];
     ip.si_m = a->sidx[1];
+    ip.skv_n = a->skv[1];
     ip.tiles_per_b = plan.tiles_per_b;
     ip.cap = plan.tile_cap;
     ip.force = (a->flags & SA_FLAG_FORCE_TILES) ? 1 : 0;
@@ -1105,7 +1182,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     tp.meta = ip.meta;
     tp.meta_out = ip.meta;
     tp.order = order;
-    tp.rows = ip.rows;
+    tp.row_off = ip.row_off;
     tp.cnts = ip.cnts;
     tp.m = a->m;
     tp.cap = plan.tile_cap;
