@@ -43,7 +43,8 @@ struct Plan {
   int64_t tiles_per_b; // ceil(m / kTileQueries)
   int64_t ntiles;      // b * tiles_per_b
   int64_t tile_cap;    // union entries stored per tile (multiple of kTileRows);
-                       // each has an int32 row and kTileQueries count bytes
+                       // each has a 32-bit row offset and kTileQueries fp16
+                       // log2 multiplicities
   size_t meta_off, order_off, rows_off, cnts_off, part_off;  // workspace byte offsets
   size_t ws_bytes;     // total workspace
 };
@@ -140,8 +141,8 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     off = round_up(off + size_t(p.ntiles) * 4, 256);
     p.rows_off = off;
     off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
-    p.cnts_off = off;
-    off = round_up(off + size_t(p.ntiles) * p.tile_cap * kTileQueries, 256);
+    p.cnts_off = off;  // fp16 log2 multiplicity per (union entry, tile query)
+    off = round_up(off + size_t(p.ntiles) * p.tile_cap * kTileQueries * 2, 256);
   }
   if (p.nsplit > 1) {
     p.part_off = off;

@@ -84,6 +84,7 @@ static_assert(kTQ == 2 * kWaves && kTileRows == 64, "shared tile wave layout");
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4_t;
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -115,7 +116,7 @@ struct IndexParams {
   int32_t* err;
   int32_t* meta;        // [ntiles][kMetaInts]
   uint32_t* row_off;    // [ntiles][cap] byte offsets of the union rows in the batch's kv
-  uint8_t* cnts;        // [ntiles][cap / 64][kTQ][64] multiplicity bytes
+  _Float16* lcnt;       // [ntiles][cap / 64][kTQ][64] log2 multiplicities (-inf: absent)
   int64_t m, kv_len, topk;
   int64_t si_b, si_m;
   int64_t skv_n;        // kv row stride (elements)
@@ -132,7 +133,7 @@ struct TileParams {
   int32_t* meta_out;    // same array: a tile that must rescale marks itself per-query
   const int32_t* order; // work-group i runs tile order[i]
   const uint32_t* row_off;
-  const uint8_t* cnts;
+  const _Float16* lcnt;
   int64_t m, cap, tiles_per_b;
   int64_t sq_b, sq_m, sq_h;
   int64_t skv_b, skv_n;
@@ -161,27 +162,22 @@ __device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// Four v_mfma_f32_32x32x16_bf16 sharing one B operand, accumulating in AGPRs.
-// Issued as inline assembly so that the compiler's own MFMAs in the same
-// kernel keep their accumulators in VGPRs (the library is built with
-// -amdgpu-mfma-vgpr-form): the shared-row kernel needs all 256 AGPRs for O
-// and 32 VGPRs for S at the same time. Hazards the compiler cannot see:
+// v_mfma_f32_32x32x16_bf16 accumulating in AGPRs, issued as inline assembly
+// so that the compiler's own MFMAs in the same kernel keep their accumulators
+// in VGPRs (the library is built with -amdgpu-mfma-vgpr-form): the shared-row
+// kernel needs all 256 AGPRs for O and 32 VGPRs for S at the same time.
+// Hazards the compiler cannot see:
 //  * a VALU write of an A/B operand register needs 2 wait states before the
 //    MFMA reads it: s_nop 2 gives 3;
 //  * back-to-back accumulation into the same registers needs none;
 //  * AGPR reads of the results (v_accvgpr_read) need the MFMA's 8 passes plus
 //    3: mfma_agpr_drain() gives 16 wait states.
-__device__ __forceinline__ void mfma4_agpr(f32x16& c0, f32x16& c1, f32x16& c2, f32x16& c3,
-                                           bf16x8 a0, bf16x8 a1, bf16x8 a2, bf16x8 a3,
-                                           bf16x8 b) {
+__device__ __forceinline__ void mfma_agpr(f32x16& c, bf16x8 a, bf16x8 b) {
   asm volatile(
       "s_nop 2\n\t"
-      "v_mfma_f32_32x32x16_bf16 %0, %4, %8, %0\n\t"
-      "v_mfma_f32_32x32x16_bf16 %1, %5, %8, %1\n\t"
-      "v_mfma_f32_32x32x16_bf16 %2, %6, %8, %2\n\t"
-      "v_mfma_f32_32x32x16_bf16 %3, %7, %8, %3"
-      : "+a"(c0), "+a"(c1), "+a"(c2), "+a"(c3)
-      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "v"(b));
+      "v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
+      : "+a"(c)
+      : "v"(a), "v"(b));
 }
 
 __device__ __forceinline__ void mfma_agpr_drain() {
@@ -496,9 +492,13 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdPara
 // ============================================================================
 // Builds, for one tile of kTQ consecutive queries, the ascending union of the
 // rows its valid slots name and each row's multiplicity in every query.
-// Count layout of a tile: for step s (64 union entries) and tile query q, the
-// 64 count bytes of the step's rows are contiguous at ((s * kTQ) + q) * 64, so
-// a lane reads the counts of 4 consecutive rows of its query as one dword.
+// Multiplicity layout of a tile: for step s (64 union entries) and tile query
+// q, the 64 values of the step's rows are contiguous at ((s * kTQ) + q) * 64.
+// A value is log2 of the row's count in the query as fp16 (exact for powers of
+// two, within 2^-11 relative otherwise) or -inf when the query does not name
+// the row, so that s * scale + value is the masked, multiplicity-weighted
+// score in the log2 domain. A lane reads 4 consecutive rows of its query as
+// 8 bytes.
 constexpr int kIdxBatch = 8;                       // index loads per thread per batch
 constexpr int kIdxBatchSlots = kIdxBatch * kThreads;
 
@@ -606,13 +606,17 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
     nU += t;
   }
   uint32_t* row_off = p.row_off + tile * p.cap;
-  uint8_t* cnts = p.cnts + tile * p.cap * kTQ;
+  _Float16* lcnt = p.lcnt + tile * p.cap * kTQ;
   const uint32_t row_bytes = uint32_t(p.skv_n) * 2u;  // the plan keeps offsets in 32 bits
   auto put = [&](int e, int row, unsigned long long w) {
     row_off[e] = uint32_t(row) * row_bytes;
-    uint8_t* cb = cnts + (e / kTileRows) * (kTQ * kTileRows) + (e % kTileRows);
+    _Float16* cb = lcnt + (e / kTileRows) * (kTQ * kTileRows) + (e % kTileRows);
 #pragma unroll
-    for (int k = 0; k < kTQ; ++k) cb[k * kTileRows] = uint8_t((w >> (8 * k)) & 255ull);
+    for (int k = 0; k < kTQ; ++k) {
+      const unsigned c = unsigned((w >> (8 * k)) & 255ull);
+      cb[k * kTileRows] = c == 0u ? static_cast<_Float16>(-INFINITY)
+                                  : static_cast<_Float16>(log2f(float(c)));
+    }
   };
   const unsigned long long below = (1ull << lane) - 1ull;  // lanes under this one
   for (int c = c_lo; c < c_hi; ++c) {
@@ -720,7 +724,7 @@ constexpr int kTileCols = kTQ * kHeads;      // 128 score columns
 __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kTilePitch];
   __shared__ __attribute__((aligned(16))) uint8_t s_p[kTileCols * kPPitch];
-  __shared__ __attribute__((aligned(16))) uint8_t s_cnt[2][kTQ * kTileRows];
+  __shared__ __attribute__((aligned(16))) _Float16 s_lc[2][kTQ * kTileRows];
   __shared__ int s_abort;
 
   const int tid = threadIdx.x;
@@ -766,7 +770,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   }
 
   const uint32_t* urows = p.row_off + tile * p.cap;
-  const uint8_t* ucnts = p.cnts + tile * p.cap * kTQ;
+  const _Float16* ulc = p.lcnt + tile * p.cap * kTQ;
   const uint8_t* kvb = reinterpret_cast<const uint8_t*>(p.kv + bi * p.skv_b);
   // LDS address of this wave's first tile row in buffer 0
   const uint32_t lds_rows = __builtin_amdgcn_readfirstlane(uint32_t(
@@ -784,10 +788,9 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     lds_dma_row(kvb + off, 16 * lane,
                 lds_rows + uint32_t(buf * kTileRows * kTilePitch + i * kTilePitch));
   };
-  // The 512 count bytes of a step (wave 0, lanes 0..31).
+  // The 1 KiB of log2 multiplicities of a step (wave 0).
   auto dma_counts = [&](int step, int buf) {
-    if (wave == 0 && lane < 32)
-      lds_dma16_async(ucnts + step * (kTQ * kTileRows) + 16 * lane, &s_cnt[buf][0]);
+    if (wave == 0) lds_dma16_async(ulc + step * (kTQ * kTileRows) + 8 * lane, &s_lc[buf][0]);
   };
 
   float m_run = -INFINITY;  // reference max of column l32 (log2 domain)
@@ -825,22 +828,22 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   uint8_t* pwrite = s_p + (32 * wave + l32) * kPPitch + 8 * hi;
 
   // Softmax of one 32-row half of a step, cut into slots that ride between
-  // MFMAs: slots 0..7 mask and scale two scores each and take the column max,
-  // slot 8 merges the max of the lane pair and checks / sets the column's
-  // reference, slots 9..24 turn one score each into c * 2^(s - m), add it to
-  // the column sum and store P as bf16 (every fourth slot).
+  // MFMAs: slots 0..7 turn two scores each into s * scale + log2 c (-inf for
+  // rows the query does not name) and take the column max, slot 8 merges the
+  // max of the lane pair and checks / sets the column's reference, slots
+  // 9..24 turn one score each into c * 2^(s - m) = 2^(x - m), add it to the
+  // column sum and store P as bf16 (every fourth slot). (v_dot2 forms of the
+  // sum stall the MFMAs they are interleaved with on gfx950: plain adds.)
   constexpr int kSmSlots = 25;
   bool abort_any = false;  // wave-uniform: a column jumped above its reference
-  auto sm_slot = [&](int k, f32x16& x, const uint32_t(&cw)[4], int rb, float& mx, float& mref,
+  auto sm_slot = [&](int k, f32x16& x, const f16x4(&lc)[4], int rb, float& mx, float& mref,
                      float& psum, bf16x4& pk) {
     if (k < 8) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int e = 2 * k + t;
-        const bool valid = ((cw[e >> 2] >> (8 * (e & 3))) & 255u) != 0u;
-        const float sv = valid ? x[e] * p.scale_log2 : -INFINITY;
-        x[e] = sv;
-        mx = fmaxf(mx, sv);
+        x[e] = fmaf(x[e], p.scale_log2, static_cast<float>(lc[e >> 2][e & 3]));
+        mx = fmaxf(mx, x[e]);
       }
     } else if (k == 8) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
@@ -854,9 +857,9 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       mref = m_run == -INFINITY ? 0.f : m_run;  // column still empty
     } else if (k < kSmSlots) {
       const int e = k - 9;
-      const float cnt = float((cw[e >> 2] >> (8 * (e & 3))) & 255u);
-      const float pj = cnt * __builtin_amdgcn_exp2f(x[e] - mref);  // 0 for masked rows
+      const float pj = __builtin_amdgcn_exp2f(x[e] - mref);  // c * 2^(s - m); 0 if masked
       psum += pj;
+      asm volatile("" : "+v"(psum));  // keep the sum in its slot (not sunk to the loop end)
       pk[e & 3] = static_cast<__bf16>(pj);
       if ((e & 3) == 3) *reinterpret_cast<bf16x4*>(pwrite + 2 * (32 * rb + 8 * (e >> 2))) = pk;
     }
@@ -865,20 +868,22 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
     const uint8_t* tb = s_tile[buf];
-    const uint8_t* cb = s_cnt[buf];
+    const _Float16* lb = s_lc[buf];
     const int nxt = min(step + 1, nsteps - 1);  // the last step refetches itself: harmless
 
-    // counts of this lane's rows in its query: rows 32rb + 8a + 4hi + (0..3)
-    uint32_t cw0[4], cw1[4];
+    // log2 multiplicities of this lane's rows in its query: rows
+    // 32rb + 8a + 4hi + (0..3)
+    f16x4 lc0[4], lc1[4];
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      cw0[a] = *reinterpret_cast<const uint32_t*>(&cb[qw * kTileRows + 8 * a + 4 * hi]);
-      cw1[a] = *reinterpret_cast<const uint32_t*>(&cb[qw * kTileRows + 32 + 8 * a + 4 * hi]);
+      lc0[a] = *reinterpret_cast<const f16x4*>(&lb[qw * kTileRows + 8 * a + 4 * hi]);
+      lc1[a] = *reinterpret_cast<const f16x4*>(&lb[qw * kTileRows + 32 + 8 * a + 4 * hi]);
     }
 
     // ---- S^T = K . Q^T, rows 0..31 then 32..63; the softmax of rows 0..31 runs
     // between the MFMAs of rows 32..63. All 16 rows of this wave's share of the
-    // next step are gathered here, so they have the rest of the step to land.
+    // next step are gathered between the MFMAs of rows 0..31, so they have the
+    // rest of the step to land.
     f32x16 sacc0, sacc1;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -902,9 +907,9 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
           sacc0 = mfma_32x32x16(kf[i % 3], qf[i], sacc0);
         else
           sacc1 = mfma_32x32x16(kf[i % 3], qf[i - kDim / 16], sacc1);
-        if ((i & 3) == 3) dma_row(rows_next, i >> 2, buf ^ 1);
+        if (i < kDim / 16 && (i & 1) == 1) dma_row(rows_next, i >> 1, buf ^ 1);
         if (i == 1) dma_counts(nxt, buf ^ 1);
-        if (i >= kDim / 16) sm_slot(i - kDim / 16, sacc0, cw0, 0, mx, mref, psum, pk);
+        if (i >= kDim / 16) sm_slot(i - kDim / 16, sacc0, lc0, 0, mx, mref, psum, pk);
         __builtin_amdgcn_sched_barrier(0);  // keep the interleave
       }
       l_run += psum;
@@ -915,8 +920,8 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     // ---- O += P . V over 32 rows (k-blocks kb0, kb0 + 1): per k-block 4 P
     // fragments (b128, the second k-block's read during the first) and 4 V
     // fragments (2 transposing reads each) read two ahead into a 3-slot ring;
-    // each V fragment feeds 4 MFMAs. `extra(n)` is VALU work placed before the
-    // n-th group of 4 MFMAs.
+    // each V fragment feeds 4 MFMAs. `extra(j)` is VALU work issued after the
+    // j-th of the 32 MFMAs, while it executes.
     auto pv_half = [&](int kb0, auto&& extra) {
       bf16x8 af[2][4];
       bf16x8 vf[3];
@@ -940,10 +945,12 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
         const int db = n & 3;
         if (n + 2 < 8) vread(n + 2, (n + 2) % 3);
         if (n == 0) pread_kb(kb0 + 1, 1);
-        extra(n);
-        mfma4_agpr(oacc[db], oacc[4 + db], oacc[8 + db], oacc[12 + db], af[kb][0], af[kb][1],
-                   af[kb][2], af[kb][3], vf[n % 3]);
-        __builtin_amdgcn_sched_barrier(0);  // keep the read-ahead order
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          mfma_agpr(oacc[4 * c + db], af[kb][c], vf[n % 3]);
+          extra(4 * n + c);
+          __builtin_amdgcn_sched_barrier(0);  // one MFMA per slot, reads ahead in order
+        }
       }
     };
 
@@ -951,11 +958,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     {
       float mx = -INFINITY, mref = 0.f, psum = 0.f;
       bf16x4 pk;
-      pv_half(0, [&](int n) {
-#pragma unroll
-        for (int k = (kSmSlots * n + 7) / 8; k < (kSmSlots * (n + 1) + 7) / 8; ++k)
-          sm_slot(k, sacc1, cw1, 1, mx, mref, psum, pk);
-      });
+      pv_half(0, [&](int j) { sm_slot(j, sacc1, lc1, 1, mx, mref, psum, pk); });
       l_run += psum;
     }
     if (abort_any) s_abort = 1;
@@ -1151,7 +1154,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     ip.err = a->err_word;
     ip.meta = reinterpret_cast<int32_t*>(ws + plan.meta_off);
     ip.row_off = reinterpret_cast<uint32_t*>(ws + plan.rows_off);
-    ip.cnts = ws + plan.cnts_off;
+    ip.lcnt = reinterpret_cast<_Float16*>(ws + plan.cnts_off);
     ip.m = a->m;
     ip.kv_len = a->kv_len;
     ip.topk = a->topk;
@@ -1183,7 +1186,7 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     tp.meta_out = ip.meta;
     tp.order = order;
     tp.row_off = ip.row_off;
-    tp.cnts = ip.cnts;
+    tp.lcnt = ip.lcnt;
     tp.m = a->m;
     tp.cap = plan.tile_cap;
     tp.tiles_per_b = plan.tiles_per_b;

@@ -197,9 +197,9 @@ def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
         assert p["nsplit"] == 1
         assert p["tiles_per_b"] == -(-m // 8) and p["ntiles"] == b * p["tiles_per_b"]
         assert p["tile_cap"] % 64 == 0 and p["tile_cap"] >= min(kv_len, 8 * topk)
-        # per tile: meta, its slot in the launch order, int32 rows and one
-        # count byte per (query, union row)
-        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 8) * p["tile_cap"])
+        # per tile: meta, its slot in the launch order, a 32-bit offset per
+        # union row and an fp16 log2 multiplicity per (query, union row)
+        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 2 * 8) * p["tile_cap"])
 
 
 @pytest.mark.parametrize("b,m,topk,cus,expect_ns,expect_len", [
