@@ -6,22 +6,29 @@ One "step" is one ``sparse_attn`` call over one batch of synthetic inputs
 already resident in HBM. The default workload is the causal-prefill
 configuration (b=1, m=4096, h=16, d=512, kv_len=4096, topk=2048) that the
 headline metric is quoted on. Calls rotate over ``--sets`` distinct input
-sets (separate q/kv/idx/o buffers) so no call finds the previous call's data
-in the caches. The timed region is bracketed by ``torch.cuda.synchronize()``
-and HIP events on the stream the kernels run on (torch's current stream).
+sets (separate q/kv/o buffers) so no call finds the previous call's data in
+the caches.
 
-Printed: ONE JSON line (stdout) with the metric, the roofline of the dominant
-kernel (algorithmic flops or bytes per call / measured call time, against
-MI355X's published peaks) and a CPU baseline (this repository's torch-CPU
-restatement of the reference formula, timed on a bounded sample of the same
-workload on the host cores). ``--all`` also prints one line per
-configuration on stderr.
+Two timed loops of K calls each, both bracketed by ``torch.cuda.synchronize()``:
+  1. whole calls through the drop-in (``submission.sparse_attn``), timed with
+     HIP events on the stream the kernels run on -> ``value``, ``ms_per_step``;
+  2. the same calls through the C-ABI's event hook (``sa_forward_events``),
+     which records HIP events on that stream around every kernel it launches
+     -> the average launch duration of each kernel; the longest is the
+     dominant kernel, whose algorithmic work per launch / duration is
+     ``roofline.achieved``.
+
+Printed: ONE JSON line (stdout). ``--all`` also prints one line per other
+configuration on stderr. ``--copy-calibration`` runs a plain device copy of
+known size instead (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters).
 """
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -40,6 +47,15 @@ METRIC = ("sparse_attn µs/call, TFLOP/s + gathered-KV GB/s (% roofline) "
 PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 H, D = wl.NUM_HEADS, wl.HEAD_DIM
+KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel",
+                "tile": "sa_fwd_tile_kernel", "query": "sa_fwd_query_kernel",
+                "combine": "sa_combine_kernel"}
+
+# HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs
+# (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the same
+# counters read for a plain copy of known size (bench.py --copy-calibration).
+# Source: profiles/pmc_traffic_*.txt (commands and raw figures there).
+TRAFFIC = {}
 
 
 def algorithmic(idx_cpu: torch.Tensor, b, m):
@@ -65,7 +81,7 @@ def make_sets(name, nsets, dev):
     return cpu, sets
 
 
-def time_gpu(fn, sets, scale, steps, warmup):
+def time_calls(fn, sets, scale, steps, warmup):
     for i in range(warmup):
         s = sets[i % len(sets)]
         fn(s[0], s[1], s[2], s[3], scale)
@@ -81,8 +97,65 @@ def time_gpu(fn, sets, scale, steps, warmup):
     return start.elapsed_time(end) / steps  # ms per call
 
 
-def cpu_baseline(cpu_inputs, target_s=10.0):
-    """Time the torch-CPU restatement on a bounded sample of queries."""
+def kernel_times(sets, scale, steps, warmup):
+    """Average launch duration (ms) of each kernel over `steps` calls, from
+    the HIP events sa_forward_events records on the calls' stream, and the
+    per-tile modes of the last call (None without a shared-row plan)."""
+    import sa_capi
+    lib = sa_capi.load()
+    stream = torch.cuda.current_stream()
+    outs = [torch.empty_like(s[0]) for s in sets]
+    args = [sa_capi.make_args(s[0], s[1], s[2], s[3], o, scale) for s, o in zip(sets, outs)]
+    wsz = max(sa_capi.workspace_bytes(lib, a) for a in args)
+    ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device=sets[0][0].device)
+    for a in args:
+        a.workspace, a.workspace_bytes = ws.data_ptr(), wsz
+    nk = sa_capi.SA_KERNEL_COUNT
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nk)] for _ in range(steps)]
+    for row in evs:          # torch creates the HIP event at its first record
+        for e in row:
+            e.record(stream)
+    for i in range(warmup):
+        sa_capi.check(lib, lib.sa_forward(ctypes.byref(args[i % len(args)]),
+                                          ctypes.c_void_p(stream.cuda_stream)), "sa_forward")
+    torch.cuda.synchronize()
+    masks = [sa_capi.forward_events(lib, args[i % len(args)], stream.cuda_stream, evs[i])
+             for i in range(steps)]
+    torch.cuda.synchronize()
+    times = {}
+    for k, name in enumerate(sa_capi.KERNELS):
+        d = [evs[i][2 * k].elapsed_time(evs[i][2 * k + 1]) for i in range(steps)
+             if (masks[i] >> k) & 1]
+        if d:
+            times[name] = sum(d) / len(d)
+    modes = None
+    if "tile" in times:      # the index kernel's per-tile meta sits at workspace offset 0
+        q = sets[0][0]
+        ntiles = q.shape[0] * ((q.shape[1] + 7) // 8)
+        modes = ws[: ntiles * 16].view(torch.int32).view(ntiles, 4)[:, 1].cpu()
+    return times, modes
+
+
+def kernel_share(idx_cpu, modes, kernel):
+    """Valid slots processed by `kernel` ("tile" or "query") in the last call."""
+    valid = (idx_cpu != -1).sum(dim=2)                  # [b, m]
+    n_all = int(valid.sum())
+    if modes is None:
+        return n_all if kernel != "tile" else 0
+    b, m = valid.shape
+    tpb = (m + 7) // 8
+    shared = torch.zeros(b, m, dtype=torch.bool)
+    for t in torch.nonzero(modes == 1).flatten().tolist():
+        bi, j = divmod(t, tpb)
+        shared[bi, 8 * j: 8 * j + 8] = True
+    n_tile = int(valid[shared].sum())
+    return n_tile if kernel == "tile" else n_all - n_tile
+
+
+def cpu_baseline(cpu_inputs, target_s=4.0, runs=3):
+    """Time the torch-CPU restatement on a bounded random sample of queries:
+    the sample is sized to about `target_s` seconds, then timed `runs` times
+    (median)."""
     from oracle import sparse_attn_ref
     q, kv, sink, idx, scale = cpu_inputs
     b, m = q.shape[0], q.shape[1]
@@ -103,16 +176,44 @@ def cpu_baseline(cpu_inputs, target_s=10.0):
     run(min(2, b * m))                                   # warmup
     nq = min(b * m, 4)
     dt, nv = run(nq)
-    while dt < target_s / 4 and nq < b * m:              # grow to the target
+    while dt < target_s / 2 and nq < b * m:              # grow to the target
         nq = min(b * m, max(nq + 1, int(nq * target_s / max(dt, 1e-3))))
         dt, nv = run(nq)
+    dts = [dt] + [run(nq)[0] for _ in range(runs - 1)]
+    dt = statistics.median(dts)
     flops = 4.0 * H * D * nv
     return {"value": round(flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": (f"{nq} of {b * m} queries (random, seed 7) of the same inputs, "
-                       f"{nv} valid slots, {dt:.2f} s, torch-CPU restatement of "
-                       f"reference.py:24-40, one query per call"),
+                       f"{nv} valid slots; median of {runs} runs of {dt:.2f} s; torch-CPU "
+                       f"restatement of reference.py:24-40 (oracle/sparse_attn_ref.py), "
+                       f"one query per call, {threads} threads"),
             "us_per_call_extrapolated": round(dt / nq * b * m * 1e6, 1)}
+
+
+def roofline(name, idx_cpu, b, m, flops, compulsory, n_valid, times, modes):
+    dom = max(times, key=times.get)
+    t = times[dom] * 1e-3
+    mfma_bound = flops / (PEAK_MFMA_TFLOPS * 1e12) >= compulsory / (PEAK_HBM_GBPS * 1e9)
+    share = 0.0
+    if dom in ("tile", "query"):
+        share = kernel_share(idx_cpu, modes, dom) / max(n_valid, 1)
+    elif dom == "combine":
+        share = 1.0
+    if mfma_bound:
+        ach = flops * share / t / 1e12
+        roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_MFMA_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_TFLOPS, 4)}
+    else:
+        ach = compulsory * share / t / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
+                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4)}
+    roof["traffic"] = TRAFFIC.get(name)
+    roof["kernel"] = KERNEL_NAMES[dom]
+    roof["kernel_us"] = round(times[dom] * 1e3, 2)
+    roof["work_share"] = round(share, 4)
+    roof["kernel_us_all"] = {KERNEL_NAMES[k]: round(v * 1e3, 2) for k, v in times.items()}
+    return roof
 
 
 def bench_config(name, steps, warmup, nsets, with_cpu):
@@ -125,21 +226,11 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
     b, m = q.shape[0], q.shape[1]
     cfg = wl.CONFIGS[name]
     n_valid, flops, gathered, uniq, compulsory = algorithmic(idx, b, m)
-    ms = time_gpu(submission.sparse_attn, sets, scale, steps, warmup)
+    ms = time_calls(submission.sparse_attn, sets, scale, steps, warmup)
+    times, modes = kernel_times(sets, scale, steps, warmup)
     t = ms * 1e-3
     tflops = flops / t / 1e12
     gbps = gathered / t / 1e9
-    t_mfma = flops / (PEAK_MFMA_TFLOPS * 1e12)
-    t_hbm = compulsory / (PEAK_HBM_GBPS * 1e9)
-    if t_mfma >= t_hbm:
-        roof = {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(tflops / PEAK_MFMA_TFLOPS, 4)}
-    else:
-        ach = compulsory / t / 1e9
-        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
-                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4)}
-    roof["traffic"] = None
-    roof["kernel"] = "sa_fwd_kernel" + (" + sa_combine_kernel" if b * m < 256 else "")
     rec = {
         "metric": METRIC,
         "value": round(tflops, 3),
@@ -162,15 +253,26 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
                    "n_valid": n_valid, "unique_rows": uniq,
                    "flops_alg": flops, "gathered_bytes": gathered,
                    "compulsory_bytes": compulsory, "input_sets_rotated": nsets},
-        "roofline": roof,
+        "roofline": roofline(name, idx, b, m, flops, compulsory, n_valid, times, modes),
     }
-    if with_cpu:
-        rec["cpu_baseline"] = cpu_baseline(cpu_inputs)
-    else:
-        rec["cpu_baseline"] = None
+    rec["cpu_baseline"] = cpu_baseline(cpu_inputs) if with_cpu else None
     del sets
     torch.cuda.empty_cache()
     return rec
+
+
+def copy_calibration(mib=1024, reps=5):
+    """A plain device-to-device copy of `mib` MiB, `reps` times: under
+    rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch scale the
+    counters of the other kernels to bytes."""
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n * 4, "reps": reps}), flush=True)
 
 
 def main():
@@ -182,6 +284,8 @@ def main():
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--all", action="store_true", help="also bench every config (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain copy of known size (PMC byte scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (sparse_attn has no multi-GPU "
@@ -190,12 +294,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration()
+        return
     if args.all:
         for name in wl.CONFIGS:
             if name == args.config:
                 continue
-            sets = args.sets if name != "decode" else min(args.sets, 4)
-            rec = bench_config(name, args.steps, args.warmup, sets, with_cpu=False)
+            rec = bench_config(name, args.steps, args.warmup, args.sets, with_cpu=False)
             print(json.dumps(rec), file=sys.stderr, flush=True)
     rec = bench_config(args.config, args.steps, args.warmup, args.sets,
                        with_cpu=not args.no_cpu)

@@ -102,6 +102,29 @@ int sa_workspace_bytes(const sa_args* a, size_t* out_bytes);
  */
 int sa_forward(const sa_args* a, void* hip_stream);
 
+/* Kernels of one sa_forward call, in launch order. */
+enum {
+  SA_KERNEL_INDEX = 0,    /* row unions of shared-row tiles (tile plans)   */
+  SA_KERNEL_ORDER = 1,    /* longest-first tile order (tile plans)         */
+  SA_KERNEL_TILE = 2,     /* shared-row tiles (tile plans)                 */
+  SA_KERNEL_QUERY = 3,    /* per-query parts (every plan)                  */
+  SA_KERNEL_COMBINE = 4,  /* merge of split-topk parts (split plans)       */
+  SA_KERNEL_COUNT = 5
+};
+
+/*
+ * Measurement hook. No counterpart in the reference, which times whole calls
+ * from Python (track-01/bench.py:20-47). Same as sa_forward, and also records
+ * events[2k] on hip_stream immediately before kernel k is launched and
+ * events[2k + 1] immediately after it, for every kernel the call launches.
+ * `events` holds 2 * SA_KERNEL_COUNT of the caller's hipEvent_t handles
+ * (created with timing enabled; NULL entries are skipped). Bit k of
+ * *launched (if non-null) is set when kernel k was launched. Nothing
+ * synchronizes: read the events once the stream has drained.
+ */
+int sa_forward_events(const sa_args* a, void* hip_stream, void* const* events,
+                      uint32_t* launched);
+
 /* Static description of a return code. */
 const char* sa_strerror(int code);
 

@@ -1078,6 +1078,8 @@ int current_cus(int* cus) {
   return SA_OK;
 }
 
+int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched);
+
 }  // namespace
 
 extern "C" {
@@ -1109,6 +1111,22 @@ int sa_workspace_bytes(const sa_args* a, size_t* out_bytes) {
 }
 
 int sa_forward(const sa_args* a, void* hip_stream) {
+  return forward(a, static_cast<hipStream_t>(hip_stream), nullptr, nullptr);
+}
+
+int sa_forward_events(const sa_args* a, void* hip_stream, void* const* events,
+                      uint32_t* launched) {
+  if (launched != nullptr) *launched = 0u;
+  return forward(a, static_cast<hipStream_t>(hip_stream), events, launched);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The launches of one call. With `events`, records events[2k] / events[2k+1]
+// on the stream around kernel k (SA_KERNEL_*) and sets bit k of *launched.
+int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched) {
   const int rc = sa::validate(a);
   if (rc != SA_OK) return rc;
   if (a->b == 0 || a->m == 0) return SA_OK;
@@ -1118,7 +1136,12 @@ int sa_forward(const sa_args* a, void* hip_stream) {
   const sa::Plan plan = sa::make_plan(a, cus);
   if (plan.ws_bytes > 0 && (a->workspace == nullptr || a->workspace_bytes < plan.ws_bytes))
     return SA_EWORKSPACE;
-  hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  auto mark = [&](int k, int after) -> bool {
+    if (after && launched != nullptr) *launched |= 1u << k;
+    if (events == nullptr) return true;
+    hipEvent_t ev = static_cast<hipEvent_t>(events[2 * k + after]);
+    return ev == nullptr || hipEventRecord(ev, stream) == hipSuccess;
+  };
   uint8_t* ws = static_cast<uint8_t*>(a->workspace);
   const float scale_log2 = a->scale * kLog2e;
 
@@ -1169,13 +1192,17 @@ int sa_forward(const sa_args* a, void* hip_stream) {
         hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
       return SA_EHIP;
+    if (!mark(SA_KERNEL_INDEX, 0)) return SA_EHIP;
     hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), lds,
                        stream, ip);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
+    if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
     int32_t* order = reinterpret_cast<int32_t*>(ws + plan.order_off);
+    if (!mark(SA_KERNEL_ORDER, 0)) return SA_EHIP;
     hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream,
                        static_cast<const int32_t*>(ip.meta), order, int(plan.ntiles));
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
+    if (!mark(SA_KERNEL_ORDER, 1)) return SA_EHIP;
 
     TileParams tp{};
     tp.q = p.q;
@@ -1200,16 +1227,20 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     tp.so_h = p.so_h;
     tp.scale_log2 = scale_log2;
     tp.nblocks = plan.ntiles;
+    if (!mark(SA_KERNEL_TILE, 0)) return SA_EHIP;
     hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), 0,
                        stream, tp);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
+    if (!mark(SA_KERNEL_TILE, 1)) return SA_EHIP;
     p.tile_meta = ip.meta;
     p.tiles_per_b = plan.tiles_per_b;
   }
 
+  if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
   hipLaunchKernelGGL(sa_fwd_query_kernel, dim3(unsigned(p.nblocks)), dim3(kThreads), 0, stream,
                      p);
   if (hipGetLastError() != hipSuccess) return SA_EHIP;
+  if (!mark(SA_KERNEL_QUERY, 1)) return SA_EHIP;
   if (plan.nsplit > 1) {
     CombineParams c{};
     c.part = p.part;
@@ -1220,11 +1251,14 @@ int sa_forward(const sa_args* a, void* hip_stream) {
     c.so_m = a->so[1];
     c.so_h = a->so[2];
     c.nsplit = plan.nsplit;
+    if (!mark(SA_KERNEL_COMBINE, 0)) return SA_EHIP;
     hipLaunchKernelGGL(sa_combine_kernel, dim3(unsigned(plan.units * kHeads)), dim3(64), 0,
                        stream, c);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
+    if (!mark(SA_KERNEL_COMBINE, 1)) return SA_EHIP;
   }
   return SA_OK;
 }
 
-}  // extern "C"
+}  // namespace
+

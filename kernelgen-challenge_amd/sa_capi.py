@@ -1,0 +1,94 @@
+"""ctypes binding of the C-ABI declared in ``include/sparse_attn.h``.
+
+The HIP library ``lib/libsparse_attn_gfx950.so`` is plain C: a Python caller
+of the reference's ``sparse_attn`` (track-01/submission.py:975) can reach it
+with this binding alone, without the torch operator. ``bench.py`` uses it for
+the per-kernel event hook ``sa_forward_events``.
+
+Tensors are torch tensors on the current HIP device; only their data pointers,
+shapes and strides cross the boundary.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libsparse_attn_gfx950.so")
+
+SA_OK, SA_EINVAL, SA_EUNSUPPORTED, SA_EWORKSPACE, SA_EHIP = range(5)
+SA_FLAG_PER_QUERY, SA_FLAG_FORCE_TILES = 1, 2
+KERNELS = ("index", "order", "tile", "query", "combine")  # SA_KERNEL_* order
+SA_KERNEL_COUNT = len(KERNELS)
+
+
+class SaArgs(ctypes.Structure):
+    """``struct sa_args`` (include/sparse_attn.h)."""
+    _fields_ = [
+        ("q", ctypes.c_void_p), ("kv", ctypes.c_void_p), ("sink", ctypes.c_void_p),
+        ("idx", ctypes.c_void_p), ("o", ctypes.c_void_p),
+        ("b", ctypes.c_int64), ("m", ctypes.c_int64), ("h", ctypes.c_int64),
+        ("d", ctypes.c_int64), ("kv_len", ctypes.c_int64), ("topk", ctypes.c_int64),
+        ("sq", ctypes.c_int64 * 4), ("skv", ctypes.c_int64 * 3),
+        ("sidx", ctypes.c_int64 * 3), ("so", ctypes.c_int64 * 4),
+        ("scale", ctypes.c_float), ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t), ("err_word", ctypes.c_void_p),
+        ("flags", ctypes.c_uint32),
+    ]
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the library and declare every entry point's signature."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    args_p = ctypes.POINTER(SaArgs)
+    lib.sa_abi_version.restype = ctypes.c_int
+    lib.sa_abi_version.argtypes = []
+    lib.sa_workspace_bytes.argtypes = [args_p, ctypes.POINTER(ctypes.c_size_t)]
+    lib.sa_forward.argtypes = [args_p, ctypes.c_void_p]
+    lib.sa_forward_events.argtypes = [args_p, ctypes.c_void_p,
+                                      ctypes.POINTER(ctypes.c_void_p),
+                                      ctypes.POINTER(ctypes.c_uint32)]
+    lib.sa_strerror.restype = ctypes.c_char_p
+    lib.sa_strerror.argtypes = [ctypes.c_int]
+    return lib
+
+
+def make_args(q, kv, sink, idx, o, scale: float, flags: int = 0, err=None) -> SaArgs:
+    """sa_args for torch tensors q [b,m,h,d], kv [b,n,d], sink [h], idx [b,m,k], o like q."""
+    a = SaArgs()
+    a.q, a.kv, a.sink = q.data_ptr(), kv.data_ptr(), sink.data_ptr()
+    a.idx, a.o = idx.data_ptr(), o.data_ptr()
+    a.b, a.m, a.h, a.d = q.shape
+    a.kv_len, a.topk = kv.shape[1], idx.shape[2]
+    a.sq[:] = list(q.stride())
+    a.skv[:] = list(kv.stride())
+    a.sidx[:] = list(idx.stride())
+    a.so[:] = list(o.stride())
+    a.scale = float(scale)
+    a.err_word = err.data_ptr() if err is not None else None
+    a.flags = flags
+    return a
+
+
+def check(lib: ctypes.CDLL, rc: int, what: str) -> None:
+    if rc != SA_OK:
+        raise RuntimeError(f"{what}: {lib.sa_strerror(rc).decode()} (code {rc})")
+
+
+def workspace_bytes(lib: ctypes.CDLL, a: SaArgs) -> int:
+    n = ctypes.c_size_t(0)
+    check(lib, lib.sa_workspace_bytes(ctypes.byref(a), ctypes.byref(n)), "sa_workspace_bytes")
+    return n.value
+
+
+def forward_events(lib: ctypes.CDLL, a: SaArgs, stream: int, events) -> int:
+    """sa_forward_events with 2 * SA_KERNEL_COUNT torch.cuda.Event objects
+    (or None entries); returns the bit mask of launched kernels."""
+    handles = (ctypes.c_void_p * (2 * SA_KERNEL_COUNT))(
+        *[(ev.cuda_event if ev is not None else None) for ev in events])
+    launched = ctypes.c_uint32(0)
+    check(lib, lib.sa_forward_events(ctypes.byref(a), ctypes.c_void_p(stream), handles,
+                                     ctypes.byref(launched)), "sa_forward_events")
+    return launched.value

@@ -83,8 +83,39 @@ def declared_functions():
 
 
 def test_header_declares_expected_api():
-    assert declared_functions() == ["sa_abi_version", "sa_forward", "sa_strerror",
-                                    "sa_workspace_bytes"]
+    assert declared_functions() == ["sa_abi_version", "sa_forward", "sa_forward_events",
+                                    "sa_strerror", "sa_workspace_bytes"]
+
+
+def test_ctypes_binding_matches_header_layout():
+    """The package's ctypes binding (sa_capi) lays sa_args out like this
+    test's own transcription of the header."""
+    import sys
+    sys.path.insert(0, PKG)
+    import sa_capi
+    assert ctypes.sizeof(sa_capi.SaArgs) == ctypes.sizeof(SaArgs)
+    for (n1, _), (n2, _) in zip(sa_capi.SaArgs._fields_, SaArgs._fields_):
+        assert n1 == n2 and getattr(sa_capi.SaArgs, n1).offset == getattr(SaArgs, n2).offset
+    assert sa_capi.KERNELS == ("index", "order", "tile", "query", "combine")
+    text = open(HEADER).read()
+    assert "SA_KERNEL_COUNT = 5" in text
+
+
+def test_forward_events_rejects_bad_args_without_device_work(libs):
+    hip, _ = libs
+    hip.sa_forward_events.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_void_p,
+                                      ctypes.POINTER(ctypes.c_void_p),
+                                      ctypes.POINTER(ctypes.c_uint32)]
+    launched = ctypes.c_uint32(7)
+    a = good_args()
+    a.h = 8
+    assert hip.sa_forward_events(ctypes.byref(a), None, None, ctypes.byref(launched)) == \
+        SA_EUNSUPPORTED
+    assert launched.value == 0
+    a = good_args()
+    a.b = 0                                     # empty: nothing launched, no events
+    assert hip.sa_forward_events(ctypes.byref(a), None, None, ctypes.byref(launched)) == SA_OK
+    assert launched.value == 0
 
 
 def test_library_exports_every_declared_symbol(libs):
