@@ -53,9 +53,11 @@ KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel"
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the same
-# counters read for a plain copy of known size (bench.py --copy-calibration).
-# Source: profiles/pmc_traffic_*.txt (commands and raw figures there).
-TRAFFIC = {}
+# counters read for a plain copy of known size (bench.py --copy-calibration:
+# FETCH_SIZE x 2.0000, WRITE_SIZE x 1.0000). Commands and raw figures:
+# profiles/sa_fwd_tile_kernel_causal_prefill_pmc_traffic.txt. Measured for
+# the kernels as built; a workload without an entry reports null.
+TRAFFIC = {"causal_prefill": 206243421}
 
 
 def algorithmic(idx_cpu: torch.Tensor, b, m):
