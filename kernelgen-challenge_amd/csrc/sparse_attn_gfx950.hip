@@ -14,6 +14,21 @@
 //
 // Kernels
 // -------
+// sa_tile_index_kernel  one work-group per tile of 8 consecutive queries of a
+//   batch: counts every valid index of the tile's queries in an LDS table
+//   (one byte per query), writes the row union in ascending order (32-bit
+//   byte offsets) with an fp16 log2 multiplicity per (query, row), and marks
+//   the tile "shared" when the dense (query x union row) work is at most 3x
+//   its valid slots, else "per query".
+// sa_tile_order_kernel  one work-group: counting sort of the tiles by
+//   descending step count, so the longest tiles are launched first.
+// sa_fwd_tile_kernel  one work-group per shared tile (128 query-head
+//   columns): gathers each union row once (LDS-DMA, 1 KiB per instruction),
+//   S^T = K . Q^T with each wave owning two queries, P through LDS, O += P . V
+//   with each wave owning a quarter of d; v_mfma_f32_32x32x16_bf16; the
+//   softmax of one 32-row half runs between the MFMAs of the next. A fixed
+//   per-column reference replaces rescaling; a tile whose scores jump above
+//   it hands itself to the per-query kernel.
 // sa_fwd_query_kernel  one work-group (4 wave64s) per (query, topk part):
 //   compacts the part's valid indices into LDS, then loops over tiles of 64
 //   gathered rows double-buffered in LDS (each row one coalesced 1 KiB wave
@@ -23,18 +38,8 @@
 //   the waves through LDS; O += P . V with the same MFMA (wave w: d columns
 //   128w..), its V operands read from the same LDS rows by
 //   ds_read_b64_tr_b16 transposing reads. Writes bf16 o, or per-part
-//   (max, sum, unnormalised O) for sa_combine_kernel.
-// sa_tile_index_kernel  one work-group per tile of 4 consecutive queries:
-//   counts every valid index of the tile's queries in an LDS table (one byte
-//   per query), compacts the row union in ascending order with the packed
-//   counts, and marks the tile "shared" when the union is small enough that
-//   computing every (query, union row) pair wastes at most half the MFMA
-//   work; otherwise "per query".
-// sa_fwd_tile_kernel  one work-group per shared tile: gathers each union row
-//   once (LDS-DMA, 1 KiB per wave instruction) and computes all 64
-//   (query, head) columns against it: S^T = K . Q^T and O += P . V with
-//   v_mfma_f32_32x32x16_bf16; a row's multiplicity c enters as + log2(c) on
-//   its score (c = 0 masks it).
+//   (max, sum, unnormalised O) for sa_combine_kernel. Skips queries of
+//   shared tiles.
 // sa_combine_kernel  merges the topk parts of one (query, head), folds the
 //   sink and stores bf16.
 #include <hip/hip_runtime.h>
