@@ -173,13 +173,13 @@ __device__ __forceinline__ f32x16 mfma_32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
 // kernel needs all 256 AGPRs for O and 32 VGPRs for S at the same time.
 // Hazards the compiler cannot see:
 //  * a VALU write of an A/B operand register needs 2 wait states before the
-//    MFMA reads it: s_nop 2 gives 3;
+//    MFMA reads it: s_nop 1 gives them;
 //  * back-to-back accumulation into the same registers needs none;
 //  * AGPR reads of the results (v_accvgpr_read) need the MFMA's 8 passes plus
 //    3: mfma_agpr_drain() gives 16 wait states.
 __device__ __forceinline__ void mfma_agpr(f32x16& c, bf16x8 a, bf16x8 b) {
   asm volatile(
-      "s_nop 2\n\t"
+      "s_nop 1\n\t"
       "v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0"
       : "+a"(c)
       : "v"(a), "v"(b));
@@ -720,9 +720,11 @@ constexpr int kTilePitch = kRowBytes + 48;
 //  * O = P . V: wave w owns d = 128w..128w+127 of all 128 columns (16 blocks
 //    of 32 x 32 fp32 in AGPRs). Each wave reads P (16 KiB) and its quarter of
 //    V (16 KiB) per step instead of all of V (64 KiB).
-//      block (cb, db): rows are columns 32cb + 8(i/4) + 4hi + i%4 (register
-//      i), MFMA column l32 is d = 128w + 32db + l32.
-// Barriers per step: one after P is written (LDS only) and the gather's.
+//      accumulator 4k + db: rows are columns 32cb + 8(i/4) + 4hi + i%4 with
+//      cb = (w + k) & 3 (register i; block k = 0 is the wave's own columns),
+//      MFMA column l32 is d = 128w + 32db + l32.
+// Barriers per step: one after each half of P is written (LDS only) and the
+// gather's.
 constexpr int kPPitch = 2 * kTileRows + 16;  // bytes per P column line
 constexpr int kTileCols = kTQ * kHeads;      // 128 score columns
 
@@ -800,7 +802,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 
   float m_run = -INFINITY;  // reference max of column l32 (log2 domain)
   float l_run = 0.f;        // this lane's share of the column's sum
-  f32x16 oacc[kDim / 32];   // [cb * 4 + db]
+  f32x16 oacc[kDim / 32];   // [4k + db], column block (wave + k) & 3
 #pragma unroll
   for (int nb = 0; nb < kDim / 32; ++nb) {
 #pragma unroll
@@ -827,8 +829,13 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   const int j = lane & 15;
   const int voff =
       (8 * (G >> 1) + (j >> 2)) * kTilePitch + 2 * (128 * wave + 16 * (G & 1) + 4 * (j & 3));
-  // P operand (A): lane reads column 32cb + l32, rows 16kb + 8hi .. +7.
-  const uint8_t* pread = s_p + l32 * kPPitch + 16 * hi;
+  // P operand (A): for accumulator block k the lane reads column
+  // 32 * ((w + k) & 3) + l32, rows 16kb + 8hi .. +7. Block 0 is the wave's own
+  // columns, which it can read before the other waves' P is in LDS.
+  const uint8_t* prd[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    prd[k] = s_p + (32 * ((wave + k) & 3) + l32) * kPPitch + 16 * hi;
   // P store: this lane's column 32w + l32, rows 32rb + 8a + 4hi .. +3.
   uint8_t* pwrite = s_p + (32 * wave + l32) * kPPitch + 8 * hi;
 
@@ -920,20 +927,19 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       l_run += psum;
     }
     rows_next = step_rows(min(step + 2, nsteps - 1));
-    lds_barrier();  // P rows 0..31 of every column are in LDS
 
     // ---- O += P . V over 32 rows (k-blocks kb0, kb0 + 1): per k-block 4 P
     // fragments (b128, the second k-block's read during the first) and 4 V
     // fragments (2 transposing reads each) read two ahead into a 3-slot ring;
-    // each V fragment feeds 4 MFMAs. `extra(j)` is VALU work issued after the
+    // each V fragment feeds 4 MFMAs. `sync()` is the barrier that makes every
+    // wave's P of these rows visible: the first V fragments and the wave's own
+    // P columns are read before it. `extra(j)` is VALU work issued after the
     // j-th of the 32 MFMAs, while it executes.
-    auto pv_half = [&](int kb0, auto&& extra) {
+    auto pv_half = [&](int kb0, auto&& sync, auto&& extra) {
       bf16x8 af[2][4];
       bf16x8 vf[3];
-      auto pread_kb = [&](int kb, int slot) {
-#pragma unroll
-        for (int c = 0; c < 4; ++c)
-          af[slot][c] = *reinterpret_cast<const bf16x8*>(pread + c * 32 * kPPitch + 32 * kb);
+      auto pread_k = [&](int kb, int slot, int k) {
+        af[slot][k] = *reinterpret_cast<const bf16x8*>(prd[k] + 32 * kb);
       };
       auto vread = [&](int n, int slot) {
         const uint8_t* v0 = tb + voff + 16 * (kb0 + (n >> 2)) * kTilePitch + 64 * (n & 3);
@@ -941,19 +947,25 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
         const bf16x4 up = lds_read_tr16(v0 + 4 * kTilePitch);
         vf[slot] = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
       };
-      pread_kb(kb0, 0);
       vread(0, 0);
       vread(1, 1);
+      pread_k(kb0, 0, 0);
+      sync();
+#pragma unroll
+      for (int k = 1; k < 4; ++k) pread_k(kb0, 0, k);
 #pragma unroll
       for (int n = 0; n < 8; ++n) {
         const int kb = n >> 2;
         const int db = n & 3;
         if (n + 2 < 8) vread(n + 2, (n + 2) % 3);
-        if (n == 0) pread_kb(kb0 + 1, 1);
+        if (n == 0) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          mfma_agpr(oacc[4 * c + db], af[kb][c], vf[n % 3]);
-          extra(4 * n + c);
+          for (int k = 0; k < 4; ++k) pread_k(kb0 + 1, 1, k);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          mfma_agpr(oacc[4 * k + db], af[kb][k], vf[n % 3]);
+          extra(4 * n + k);
           __builtin_amdgcn_sched_barrier(0);  // one MFMA per slot, reads ahead in order
         }
       }
@@ -963,15 +975,20 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     {
       float mx = -INFINITY, mref = 0.f, psum = 0.f;
       bf16x4 pk;
-      pv_half(0, [&](int j) { sm_slot(j, sacc1, lc1, 1, mx, mref, psum, pk); });
+      pv_half(0, [&]() { lds_barrier(); },  // P rows 0..31 of every column are in LDS
+              [&](int j) { sm_slot(j, sacc1, lc1, 1, mx, mref, psum, pk); });
       l_run += psum;
     }
-    if (abort_any) s_abort = 1;
-    lds_barrier();  // P rows 32..63 are in LDS; every abort of this step is set
-    const int abort_seen = s_abort;
 
     // ---- O += P . V, rows 32..63 -------------------------------------------------
-    pv_half(2, [](int) {});
+    int abort_seen = 0;
+    pv_half(2,
+            [&]() {
+              if (abort_any) s_abort = 1;
+              lds_barrier();  // P rows 32..63 are in LDS; every abort of this step is set
+              abort_seen = s_abort;
+            },
+            [](int) {});
 
     dma_barrier();  // every wave's prefetch has landed; P and this tile are free
     if (abort_seen != 0) {  // uniform: every wave read it after the same barrier
@@ -997,10 +1014,10 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   lds_barrier();
   __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + 128 * wave + l32;
 #pragma unroll
-  for (int c = 0; c < 4; ++c)
+  for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      const int col0 = 32 * c + 8 * a + 4 * hi;  // columns col0 .. col0 + 3
+      const int col0 = 32 * ((wave + k) & 3) + 8 * a + 4 * hi;  // columns col0 .. col0 + 3
       const f32x4 fs = *reinterpret_cast<const f32x4*>(&s_f[col0]);
       const int q2 = col0 >> 4;
       if (q2 < qt) {
@@ -1009,7 +1026,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
           __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t((col0 + b) & 15) * p.so_h;
 #pragma unroll
           for (int db = 0; db < 4; ++db)
-            orow[32 * db] = static_cast<__bf16>(oacc[4 * c + db][4 * a + b] * fs[b]);
+            orow[32 * db] = static_cast<__bf16>(oacc[4 * k + db][4 * a + b] * fs[b]);
         }
       }
     }
