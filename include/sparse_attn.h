@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 1
+#define SA_ABI_VERSION 2
 
 /* Return codes. */
 enum {
@@ -78,7 +78,22 @@ typedef struct sa_args {
   size_t workspace_bytes;
   int32_t* err_word;      /* device int32, nullable; bit 0 = bad index seen */
   uint32_t flags;         /* SA_FLAG_* bits, normally 0 */
+  float* lse;             /* fp32 [b, m, h], nullable: log-sum-exp per (query, head) */
+  int64_t slse[3];        /* strides of lse */
 } sa_args;
+
+/*
+ * lse (when sa_args.lse is set): for each (b, m, h), in natural log,
+ *
+ *   lse = ln( sum_t exp(s_t) + exp(sink[h]) )
+ *
+ * over the valid slots, so that o = sum_t exp(s_t - lse) * kv[idx_t]. This is
+ * m_total + ln(l_total) of the reference kernel's sink fold
+ * (track-01/submission.py:195-199, notes.md:32-41). A query with no mass at
+ * all (no valid slot and sink = -inf) gets o = 0 and lse = -inf.
+ *
+ * Version 2 added lse / slse at the end of sa_args and sa_merge.
+ */
 
 /* Version of this ABI (SA_ABI_VERSION). */
 int sa_abi_version(void);
@@ -101,6 +116,41 @@ int sa_workspace_bytes(const sa_args* a, size_t* out_bytes);
  * Argument errors return before any device work.
  */
 int sa_forward(const sa_args* a, void* hip_stream);
+
+/*
+ * Merge of partial results: parts i = 0..n-1 hold attention over disjoint
+ * subsets of a query's slots (for example KV shards), each computed with
+ * sink = -inf and returned with its lse. The merge folds the sink once:
+ *
+ *   lse = ln( sum_i exp(lse_i) + exp(sink[h]) )
+ *   o   = sum_i exp(lse_i - lse) * o_i
+ *
+ * which equals sa_forward over the union of the parts' slots (the split-topk
+ * combine of this library, exposed as its own op; the sink algebra of
+ * track-01/notes.md:32-41). A part with lse_i = -inf contributes nothing.
+ * No counterpart in the reference, which always runs the whole top-k in one
+ * kernel.
+ */
+typedef struct sa_merge_args {
+  const void* o_parts;     /* bf16 [n, b, m, h, d] */
+  const float* lse_parts;  /* fp32 [n, b, m, h]    */
+  const float* sink;       /* fp32 [h], nullable (= -inf: no sink) */
+  void* o;                 /* bf16 [b, m, h, d]  (written) */
+  float* lse;              /* fp32 [b, m, h], nullable (written) */
+  int64_t n, b, m, h, d;
+  int64_t sop[5];          /* strides of o_parts   */
+  int64_t slp[4];          /* strides of lse_parts */
+  int64_t so[4];           /* strides of o         */
+  int64_t slse[3];         /* strides of lse       */
+} sa_merge_args;
+
+/*
+ * Run the merge on `hip_stream`. d must be a multiple of 8 with unit stride;
+ * o_parts and o 16-byte aligned with their other strides multiples of 8.
+ * n = 0 writes o = 0 and lse = sink (or -inf). Asynchronous; argument errors
+ * return before any device work.
+ */
+int sa_merge(const sa_merge_args* a, void* hip_stream);
 
 /* Kernels of one sa_forward call, in launch order. */
 enum {

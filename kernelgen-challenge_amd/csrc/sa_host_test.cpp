@@ -7,6 +7,8 @@ extern "C" {
 
 int sa_host_validate(const sa_args* a) { return sa::validate(a); }
 
+int sa_host_validate_merge(const sa_merge_args* a) { return sa::validate_merge(a); }
+
 int sa_host_plan(const sa_args* a, int num_cus, int64_t* nsplit, int64_t* split_len,
                  size_t* ws_bytes) {
   const int rc = sa::validate(a);

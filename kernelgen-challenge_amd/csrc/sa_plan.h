@@ -91,7 +91,40 @@ inline int validate(const sa_args* a) {
   if (a->skv[0] < 0 || a->skv[1] < 0) return SA_EINVAL;
   if (a->sidx[0] < 0 || a->sidx[1] < 0) return SA_EINVAL;
   if (!(a->scale == a->scale)) return SA_EINVAL;  // NaN scale
+  if (a->lse != nullptr) {
+    if ((reinterpret_cast<uintptr_t>(a->lse) & 3u) != 0) return SA_EINVAL;
+    for (int i = 0; i < 3; ++i)
+      if (a->slse[i] < 0) return SA_EINVAL;
+  }
   if (a->b > kMaxUnits || a->m > kMaxUnits || a->b * a->m > kMaxUnits)
+    return SA_EUNSUPPORTED;
+  return SA_OK;
+}
+
+// Checks the arguments of sa_merge. Returns SA_OK or an error.
+inline int validate_merge(const sa_merge_args* a) {
+  if (a == nullptr) return SA_EINVAL;
+  if (a->n < 0 || a->b < 0 || a->m < 0 || a->h < 0 || a->d < 0) return SA_EINVAL;
+  if (a->b == 0 || a->m == 0 || a->h == 0 || a->d == 0) return SA_OK;  // nothing to write
+  if (a->d % 8 != 0) return SA_EINVAL;
+  if (a->o == nullptr || !aligned16(a->o) || a->so[3] != 1) return SA_EINVAL;
+  for (int i = 0; i < 3; ++i)
+    if (a->so[i] < 0 || a->so[i] % 8 != 0) return SA_EINVAL;
+  if (a->n > 0) {
+    if (a->o_parts == nullptr || a->lse_parts == nullptr) return SA_EINVAL;
+    if (!aligned16(a->o_parts) || a->sop[4] != 1) return SA_EINVAL;
+    for (int i = 0; i < 4; ++i)
+      if (a->sop[i] < 0 || a->sop[i] % 8 != 0 || a->slp[i] < 0) return SA_EINVAL;
+    if ((reinterpret_cast<uintptr_t>(a->lse_parts) & 3u) != 0) return SA_EINVAL;
+  }
+  if (a->lse != nullptr) {
+    if ((reinterpret_cast<uintptr_t>(a->lse) & 3u) != 0) return SA_EINVAL;
+    for (int i = 0; i < 3; ++i)
+      if (a->slse[i] < 0) return SA_EINVAL;
+  }
+  if (a->sink != nullptr && (reinterpret_cast<uintptr_t>(a->sink) & 3u) != 0) return SA_EINVAL;
+  if (a->b > kMaxUnits || a->m > kMaxUnits || a->h > kMaxUnits ||
+      a->b * a->m > kMaxUnits * 16 || a->b * a->m * a->h > (int64_t(1) << 31) - 1)
     return SA_EUNSUPPORTED;
   return SA_OK;
 }

@@ -1,8 +1,9 @@
 // sa_torch.cpp -- thin PyTorch-ROCm operator over the sparse_attn C-ABI.
 //
-// Registers torch.ops.sa_amd.sparse_attn_fwd. It checks devices and dtypes,
-// allocates the output (like track-01/submission.py:1000) and the split-topk
-// workspace through the caching allocator, and calls sa_forward on the
+// Registers torch.ops.sa_amd.sparse_attn_fwd (o), sparse_attn_fwd_lse
+// (o, lse) and sparse_attn_merge (o, lse of merged partials). They check
+// devices and dtypes, allocate the outputs (like track-01/submission.py:1000)
+// and the workspace through the caching allocator, and call the C-ABI on the
 // current HIP stream. No kernel code lives here.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
@@ -13,10 +14,17 @@
 
 namespace {
 
-at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
-                           const at::Tensor& attn_sink,
-                           const at::Tensor& topk_idxs, double scale,
-                           const c10::optional<at::Tensor>& err, int64_t flags) {
+void check_rc(int rc, const char* what) {
+  TORCH_CHECK_VALUE(rc != SA_EINVAL && rc != SA_EUNSUPPORTED, what, ": ", sa_strerror(rc));
+  TORCH_CHECK(rc == SA_OK, what, ": ", sa_strerror(rc));
+}
+
+// o, and lse when `want_lse` (fp32 [b, m, h]).
+std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor& kv,
+                                           const at::Tensor& attn_sink,
+                                           const at::Tensor& topk_idxs, double scale,
+                                           const c10::optional<at::Tensor>& err,
+                                           int64_t flags, bool want_lse) {
   TORCH_CHECK_VALUE(q.dim() == 4, "q must be [b, m, h, d], got ", q.sizes());
   TORCH_CHECK_VALUE(kv.dim() == 3, "kv must be [b, kv_len, d], got ", kv.sizes());
   TORCH_CHECK_VALUE(attn_sink.dim() == 1, "attn_sink must be [h], got ",
@@ -41,6 +49,7 @@ at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
   const c10::DeviceGuard guard(q.device());
   const at::Tensor sink_c = attn_sink.contiguous();
   at::Tensor o = at::empty({b, m, h, d}, q.options());
+  at::Tensor lse;
 
   sa_args a{};
   a.q = q.data_ptr();
@@ -67,23 +76,84 @@ at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
                 "err must be a contiguous int32 tensor on q's device");
     a.err_word = err->data_ptr<int32_t>();
   }
+  if (want_lse) {
+    lse = at::empty({b, m, h}, q.options().dtype(at::kFloat));
+    a.lse = lse.data_ptr<float>();
+    for (int i = 0; i < 3; ++i) a.slse[i] = lse.stride(i);
+  }
 
   size_t ws = 0;
-  int rc = sa_workspace_bytes(&a, &ws);
-  TORCH_CHECK_VALUE(rc != SA_EINVAL && rc != SA_EUNSUPPORTED,
-                    "sparse_attn: ", sa_strerror(rc));
-  TORCH_CHECK(rc == SA_OK, "sparse_attn: ", sa_strerror(rc));
+  check_rc(sa_workspace_bytes(&a, &ws), "sparse_attn");
   at::Tensor workspace;
   if (ws > 0) {
     workspace = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
     a.workspace = workspace.data_ptr();
     a.workspace_bytes = ws;
   }
-  rc = sa_forward(&a, c10::hip::getCurrentHIPStream().stream());
-  TORCH_CHECK_VALUE(rc != SA_EINVAL && rc != SA_EUNSUPPORTED,
-                    "sparse_attn: ", sa_strerror(rc));
-  TORCH_CHECK(rc == SA_OK, "sparse_attn: ", sa_strerror(rc));
-  return o;
+  check_rc(sa_forward(&a, c10::hip::getCurrentHIPStream().stream()), "sparse_attn");
+  return {o, lse};
+}
+
+at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
+                           const at::Tensor& attn_sink, const at::Tensor& topk_idxs,
+                           double scale, const c10::optional<at::Tensor>& err, int64_t flags) {
+  return std::get<0>(forward(q, kv, attn_sink, topk_idxs, scale, err, flags, false));
+}
+
+std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd_lse(
+    const at::Tensor& q, const at::Tensor& kv, const at::Tensor& attn_sink,
+    const at::Tensor& topk_idxs, double scale, const c10::optional<at::Tensor>& err,
+    int64_t flags) {
+  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, true);
+}
+
+// Merge n partials: o_parts bf16 [n, b, m, h, d], lse_parts fp32 [n, b, m, h].
+std::tuple<at::Tensor, at::Tensor> sparse_attn_merge(const at::Tensor& o_parts,
+                                                     const at::Tensor& lse_parts,
+                                                     const c10::optional<at::Tensor>& sink) {
+  TORCH_CHECK_VALUE(o_parts.dim() == 5, "o_parts must be [n, b, m, h, d], got ",
+                    o_parts.sizes());
+  TORCH_CHECK_VALUE(lse_parts.dim() == 4, "lse_parts must be [n, b, m, h], got ",
+                    lse_parts.sizes());
+  TORCH_CHECK_TYPE(o_parts.scalar_type() == at::kBFloat16, "o_parts must be bfloat16");
+  TORCH_CHECK_TYPE(lse_parts.scalar_type() == at::kFloat, "lse_parts must be float32");
+  TORCH_CHECK(o_parts.is_cuda() && lse_parts.device() == o_parts.device(),
+              "o_parts and lse_parts must be on the same GPU");
+  const int64_t n = o_parts.size(0), b = o_parts.size(1), m = o_parts.size(2),
+                h = o_parts.size(3), d = o_parts.size(4);
+  TORCH_CHECK_VALUE(lse_parts.size(0) == n && lse_parts.size(1) == b &&
+                        lse_parts.size(2) == m && lse_parts.size(3) == h,
+                    "lse_parts shape ", lse_parts.sizes(), " does not match o_parts ",
+                    o_parts.sizes());
+  const c10::DeviceGuard guard(o_parts.device());
+  const at::Tensor op = o_parts.contiguous();
+  const at::Tensor lp = lse_parts.contiguous();
+  at::Tensor sink_c;
+  if (sink.has_value()) {
+    TORCH_CHECK_TYPE(sink->scalar_type() == at::kFloat, "attn_sink must be float32");
+    TORCH_CHECK_VALUE(sink->dim() == 1 && sink->size(0) == h, "attn_sink must be [h]");
+    TORCH_CHECK(sink->device() == o_parts.device(), "attn_sink must be on the same GPU");
+    sink_c = sink->contiguous();
+  }
+  at::Tensor o = at::empty({b, m, h, d}, o_parts.options());
+  at::Tensor lse = at::empty({b, m, h}, o_parts.options().dtype(at::kFloat));
+  sa_merge_args a{};
+  a.o_parts = op.data_ptr();
+  a.lse_parts = lp.data_ptr<float>();
+  a.sink = sink.has_value() ? sink_c.data_ptr<float>() : nullptr;
+  a.o = o.data_ptr();
+  a.lse = lse.data_ptr<float>();
+  a.n = n;
+  a.b = b;
+  a.m = m;
+  a.h = h;
+  a.d = d;
+  for (int i = 0; i < 5; ++i) a.sop[i] = op.stride(i);
+  for (int i = 0; i < 4; ++i) a.slp[i] = lp.stride(i);
+  for (int i = 0; i < 4; ++i) a.so[i] = o.stride(i);
+  for (int i = 0; i < 3; ++i) a.slse[i] = lse.stride(i);
+  check_rc(sa_merge(&a, c10::hip::getCurrentHIPStream().stream()), "sparse_attn_merge");
+  return {o, lse};
 }
 
 }  // namespace
@@ -92,6 +162,15 @@ TORCH_LIBRARY(sa_amd, m) {
   m.def(
       "sparse_attn_fwd(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
       "float scale, Tensor? err=None, int flags=0) -> Tensor");
+  m.def(
+      "sparse_attn_fwd_lse(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
+      "float scale, Tensor? err=None, int flags=0) -> (Tensor, Tensor)");
+  m.def("sparse_attn_merge(Tensor o_parts, Tensor lse_parts, Tensor? attn_sink=None) -> "
+        "(Tensor, Tensor)");
 }
 
-TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) { m.impl("sparse_attn_fwd", &sparse_attn_fwd); }
+TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
+  m.impl("sparse_attn_fwd", &sparse_attn_fwd);
+  m.impl("sparse_attn_fwd_lse", &sparse_attn_fwd_lse);
+  m.impl("sparse_attn_merge", &sparse_attn_merge);
+}

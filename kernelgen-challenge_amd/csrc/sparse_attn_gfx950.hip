@@ -67,6 +67,7 @@ constexpr int kRowsPerWave = kTileRows / kWaves;  // 16
 constexpr int kDPerWave = kDim / kWaves;          // 128 output columns
 constexpr int kDBlocks = kDPerWave / 16;          // 8 MFMA column blocks
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 // Lazy rescaling: the running reference max of a softmax column moves only
 // when a tile's max exceeds it by more than this (log2 units), so exp2(s - m)
 // stays below 2^8 and the accumulators are rescaled rarely.
@@ -111,6 +112,8 @@ struct FwdParams {
   int64_t si_b, si_m;
   int64_t so_b, so_m, so_h;
   float scale_log2;     // scale * log2(e)
+  float* lse;           // fp32 [b, m, h] or null
+  int64_t sl_b, sl_m, sl_h;
   int nsplit;
   int64_t split_len;
   int64_t nblocks;      // grid size (units * nsplit)
@@ -144,6 +147,8 @@ struct TileParams {
   int64_t skv_b, skv_n;
   int64_t so_b, so_m, so_h;
   float scale_log2;
+  float* lse;           // fp32 [b, m, h] or null
+  int64_t sl_b, sl_m, sl_h;
   int64_t nblocks;
 };
 
@@ -151,9 +156,24 @@ struct CombineParams {
   const float* part;
   const float* sink;
   __bf16* o;
+  float* lse;           // fp32 [b, m, h] or null
   int64_t m;
   int64_t so_b, so_m, so_h;
+  int64_t sl_b, sl_m, sl_h;
   int nsplit;
+};
+
+struct MergeParams {
+  const __bf16* o_parts;
+  const float* lse_parts;
+  const float* sink;    // null: no sink
+  __bf16* o;
+  float* lse;
+  int64_t n, b, m, h, d;
+  int64_t sop_n, sop_b, sop_m, sop_h;
+  int64_t slp_n, slp_b, slp_m, slp_h;
+  int64_t so_b, so_m, so_h;
+  int64_t sl_b, sl_m, sl_h;
 };
 
 constexpr int64_t kPartFloats =
@@ -187,6 +207,24 @@ __device__ __forceinline__ void mfma_agpr(f32x16& c, bf16x8 a, bf16x8 b) {
 
 __device__ __forceinline__ void mfma_agpr_drain() {
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
+}
+
+// Sink fold in the log2 domain (track-01/notes.md:32-41): m, l are the max
+// (or any reference at or below it; -inf when there is no valid slot) and the
+// sum of 2^(x - m) over the valid slots, sink2 = sink * log2 e. Returns the
+// factor that turns the unnormalised output into o, and the natural-log
+// lse = ln(sum exp(s) + exp(sink)). No mass at all (no slot, sink = -inf):
+// factor 0 (o = 0) and lse = -inf.
+__device__ __forceinline__ float sink_fold(float m, float l, float sink2, float& lse) {
+  const float mt = fmaxf(m, sink2);
+  if (mt == -INFINITY) {
+    lse = -INFINITY;
+    return 0.f;
+  }
+  const float a = exp2f(m - mt);  // 0 when m = -inf
+  const float den = a * l + exp2f(sink2 - mt);
+  lse = (mt + log2f(den)) * kLn2;
+  return a / den;
 }
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the address
@@ -462,10 +500,10 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdPara
   const int dcol = wave * kDPerWave + n;
 
   if (p.nsplit == 1) {
-    const float sink2 = p.sink[n] * kLog2e;
-    const float m_tot = fmaxf(m_run, sink2);
-    const float a = exp2f(m_run - m_tot);  // 0 when no valid slot
-    const float f = a / (a * l_tot + exp2f(sink2 - m_tot));
+    float lse;
+    const float f = sink_fold(m_run, l_tot, p.sink[n] * kLog2e, lse);
+    if (p.lse != nullptr && wave == 0 && g == 0)
+      p.lse[bi * p.sl_b + mi * p.sl_m + int64_t(n) * p.sl_h] = lse;
     float fj[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) fj[j] = __shfl(f, 4 * g + j);
@@ -759,6 +797,9 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       *reinterpret_cast<bf16x8*>(ob + int64_t(qh >> 4) * p.so_m + int64_t(qh & 15) * p.so_h +
                                  8 * (i % (kDim / 8))) = z;
     }
+    if (p.lse != nullptr && tid < qt * kHeads)  // ln(exp(sink)) = sink, -inf without one
+      p.lse[bi * p.sl_b + (q0 + (tid >> 4)) * p.sl_m + int64_t(tid & 15) * p.sl_h] =
+          p.sink[tid & 15];
     return;
   }
 
@@ -1006,10 +1047,13 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run),
                                                      __float_as_uint(l_run), false, false);
     const float lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-    const float sink2 = p.sink[hh] * kLog2e;
-    const float mt = fmaxf(m_run, sink2);
-    const float a = exp2f(m_run - mt);  // 0 when the column has no valid slot
-    if (hi == 0) s_f[32 * wave + l32] = a / (a * lt + exp2f(sink2 - mt));
+    float lse;
+    const float f = sink_fold(m_run, lt, p.sink[hh] * kLog2e, lse);
+    if (hi == 0) {
+      s_f[32 * wave + l32] = f;
+      if (p.lse != nullptr && qw < qt)
+        p.lse[bi * p.sl_b + (q0 + qw) * p.sl_m + int64_t(hh) * p.sl_h] = lse;
+    }
   }
   lds_barrier();
   __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + 128 * wave + l32;
@@ -1067,14 +1111,61 @@ __global__ void __launch_bounds__(64) sa_combine_kernel(const CombineParams p) {
     acc[6] += w * v1.z;
     acc[7] += w * v1.w;
   }
-  const float sink2 = p.sink[h] * kLog2e;
-  const float m_tot = fmaxf(M, sink2);
-  const float a = exp2f(M - m_tot);
-  const float f = a / (a * L + exp2f(sink2 - m_tot));
+  float lse;
+  const float f = sink_fold(M, L, p.sink[h] * kLog2e, lse);
+  if (p.lse != nullptr && threadIdx.x == 0)
+    p.lse[bi * p.sl_b + mi * p.sl_m + int64_t(h) * p.sl_h] = lse;
   bf16x8 v;
 #pragma unroll
   for (int k = 0; k < 8; ++k) v[k] = static_cast<__bf16>(acc[k] * f);
   *reinterpret_cast<bf16x8*>(p.o + bi * p.so_b + mi * p.so_m + int64_t(h) * p.so_h + d0) = v;
+}
+
+// ============================================================================
+// merge of partial (o, lse) results: one wave64 per (b, m, h)
+// ============================================================================
+// lse = ln(sum_i exp(lse_i) + exp(sink)), o = sum_i exp(lse_i - lse) o_i, the
+// natural-log form of the split-topk combine (track-01/notes.md:32-41). Each
+// lane owns 8 consecutive d of every 512-wide chunk.
+__global__ void __launch_bounds__(256) sa_merge_kernel(const MergeParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= p.b * p.m * p.h) return;
+  const int64_t hi = row % p.h;
+  const int64_t mi = (row / p.h) % p.m;
+  const int64_t bi = row / (p.h * p.m);
+  const float* lp = p.lse_parts + bi * p.slp_b + mi * p.slp_m + hi * p.slp_h;
+  const float sink = p.sink != nullptr ? p.sink[hi] : -INFINITY;
+  float mx = sink;
+  for (int64_t i = 0; i < p.n; ++i) mx = fmaxf(mx, lp[i * p.slp_n]);
+  float lse = -INFINITY;
+  if (mx != -INFINITY) {
+    float sum = expf(sink - mx);
+    for (int64_t i = 0; i < p.n; ++i) sum += expf(lp[i * p.slp_n] - mx);
+    lse = mx + logf(sum);
+  }
+  if (p.lse != nullptr && lane == 0) p.lse[bi * p.sl_b + mi * p.sl_m + hi * p.sl_h] = lse;
+  const __bf16* op = p.o_parts + bi * p.sop_b + mi * p.sop_m + hi * p.sop_h;
+  __bf16* orow = p.o + bi * p.so_b + mi * p.so_m + hi * p.so_h;
+  for (int64_t d0 = 8 * lane; d0 < p.d; d0 += 512) {
+    float acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) acc[k] = 0.f;
+    if (lse != -INFINITY) {
+      for (int64_t i = 0; i < p.n; ++i) {
+        const float li = lp[i * p.slp_n];
+        if (li == -INFINITY) continue;  // a part without mass: its o is ignored
+        const float w = expf(li - lse);
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(op + i * p.sop_n + d0);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc[k] += w * static_cast<float>(v[k]);
+      }
+    }
+    bf16x8 out;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) out[k] = static_cast<__bf16>(acc[k]);
+    *reinterpret_cast<bf16x8*>(orow + d0) = out;
+  }
 }
 
 // Compute units of the current device, cached per device ordinal.
@@ -1142,6 +1233,41 @@ int sa_forward_events(const sa_args* a, void* hip_stream, void* const* events,
   return forward(a, static_cast<hipStream_t>(hip_stream), events, launched);
 }
 
+int sa_merge(const sa_merge_args* a, void* hip_stream) {
+  const int rc = sa::validate_merge(a);
+  if (rc != SA_OK) return rc;
+  const int64_t rows = a->b * a->m * a->h;
+  if (rows == 0 || a->d == 0) return SA_OK;
+  MergeParams p{};
+  p.o_parts = static_cast<const __bf16*>(a->o_parts);
+  p.lse_parts = a->lse_parts;
+  p.sink = a->sink;
+  p.o = static_cast<__bf16*>(a->o);
+  p.lse = a->lse;
+  p.n = a->n;
+  p.b = a->b;
+  p.m = a->m;
+  p.h = a->h;
+  p.d = a->d;
+  p.sop_n = a->sop[0];
+  p.sop_b = a->sop[1];
+  p.sop_m = a->sop[2];
+  p.sop_h = a->sop[3];
+  p.slp_n = a->slp[0];
+  p.slp_b = a->slp[1];
+  p.slp_m = a->slp[2];
+  p.slp_h = a->slp[3];
+  p.so_b = a->so[0];
+  p.so_m = a->so[1];
+  p.so_h = a->so[2];
+  p.sl_b = a->slse[0];
+  p.sl_m = a->slse[1];
+  p.sl_h = a->slse[2];
+  hipLaunchKernelGGL(sa_merge_kernel, dim3(unsigned((rows + 3) / 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(hip_stream), p);
+  return hipGetLastError() == hipSuccess ? SA_OK : SA_EHIP;
+}
+
 }  // extern "C"
 
 namespace {
@@ -1189,6 +1315,10 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
   p.so_m = a->so[1];
   p.so_h = a->so[2];
   p.scale_log2 = scale_log2;
+  p.lse = a->lse;
+  p.sl_b = a->slse[0];
+  p.sl_m = a->slse[1];
+  p.sl_h = a->slse[2];
   p.nsplit = plan.nsplit;
   p.split_len = plan.split_len;
   p.nblocks = plan.units * plan.nsplit;
@@ -1248,6 +1378,10 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.so_m = p.so_m;
     tp.so_h = p.so_h;
     tp.scale_log2 = scale_log2;
+    tp.lse = a->lse;
+    tp.sl_b = a->slse[0];
+    tp.sl_m = a->slse[1];
+    tp.sl_h = a->slse[2];
     tp.nblocks = plan.ntiles;
     if (!mark(SA_KERNEL_TILE, 0)) return SA_EHIP;
     hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), 0,
@@ -1272,6 +1406,10 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     c.so_b = a->so[0];
     c.so_m = a->so[1];
     c.so_h = a->so[2];
+    c.lse = a->lse;
+    c.sl_b = a->slse[0];
+    c.sl_m = a->slse[1];
+    c.sl_h = a->slse[2];
     c.nsplit = plan.nsplit;
     if (!mark(SA_KERNEL_COMBINE, 0)) return SA_EHIP;
     hipLaunchKernelGGL(sa_combine_kernel, dim3(unsigned(plan.units * kHeads)), dim3(64), 0,

@@ -33,7 +33,19 @@ class SaArgs(ctypes.Structure):
         ("sidx", ctypes.c_int64 * 3), ("so", ctypes.c_int64 * 4),
         ("scale", ctypes.c_float), ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t), ("err_word", ctypes.c_void_p),
-        ("flags", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32), ("lse", ctypes.c_void_p), ("slse", ctypes.c_int64 * 3),
+    ]
+
+
+class SaMergeArgs(ctypes.Structure):
+    """``struct sa_merge_args`` (include/sparse_attn.h)."""
+    _fields_ = [
+        ("o_parts", ctypes.c_void_p), ("lse_parts", ctypes.c_void_p),
+        ("sink", ctypes.c_void_p), ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("n", ctypes.c_int64), ("b", ctypes.c_int64), ("m", ctypes.c_int64),
+        ("h", ctypes.c_int64), ("d", ctypes.c_int64),
+        ("sop", ctypes.c_int64 * 5), ("slp", ctypes.c_int64 * 4),
+        ("so", ctypes.c_int64 * 4), ("slse", ctypes.c_int64 * 3),
     ]
 
 
@@ -50,13 +62,15 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sa_forward_events.argtypes = [args_p, ctypes.c_void_p,
                                       ctypes.POINTER(ctypes.c_void_p),
                                       ctypes.POINTER(ctypes.c_uint32)]
+    lib.sa_merge.argtypes = [ctypes.POINTER(SaMergeArgs), ctypes.c_void_p]
     lib.sa_strerror.restype = ctypes.c_char_p
     lib.sa_strerror.argtypes = [ctypes.c_int]
     return lib
 
 
-def make_args(q, kv, sink, idx, o, scale: float, flags: int = 0, err=None) -> SaArgs:
-    """sa_args for torch tensors q [b,m,h,d], kv [b,n,d], sink [h], idx [b,m,k], o like q."""
+def make_args(q, kv, sink, idx, o, scale: float, flags: int = 0, err=None, lse=None) -> SaArgs:
+    """sa_args for torch tensors q [b,m,h,d], kv [b,n,d], sink [h], idx [b,m,k], o like q,
+    and optionally lse fp32 [b,m,h]."""
     a = SaArgs()
     a.q, a.kv, a.sink = q.data_ptr(), kv.data_ptr(), sink.data_ptr()
     a.idx, a.o = idx.data_ptr(), o.data_ptr()
@@ -69,6 +83,9 @@ def make_args(q, kv, sink, idx, o, scale: float, flags: int = 0, err=None) -> Sa
     a.scale = float(scale)
     a.err_word = err.data_ptr() if err is not None else None
     a.flags = flags
+    if lse is not None:
+        a.lse = lse.data_ptr()
+        a.slse[:] = list(lse.stride())
     return a
 
 

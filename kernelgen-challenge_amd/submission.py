@@ -24,7 +24,7 @@ import threading
 
 import torch
 
-__all__ = ["sparse_attn", "set_index_check", "index_check_enabled", "set_path_flags",
+__all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "set_index_check", "index_check_enabled", "set_path_flags",
            "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES"]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -75,6 +75,23 @@ def set_path_flags(flags: int) -> None:
     _flags = int(flags)
 
 
+def _checked_inputs(q, kv, attn_sink, topk_idxs):
+    if q.dim() != 4:
+        raise ValueError(f"q must be 4-D [b, m, h, d], got shape {tuple(q.shape)}")
+    if kv.dim() != 3 or attn_sink.dim() != 1 or topk_idxs.dim() != 3:
+        raise ValueError("expected kv [b, kv_len, d], attn_sink [h], topk_idxs [b, m, topk]")
+    if not (q.is_cuda and kv.is_cuda and attn_sink.is_cuda and topk_idxs.is_cuda):
+        raise ValueError("sparse_attn runs on the GPU only; move all inputs to the device")
+    load_extension()
+    # Same input handling as track-01/submission.py:995-998.
+    return q.contiguous(), kv.contiguous(), attn_sink.contiguous(), topk_idxs.contiguous()
+
+
+def _raise_if_bad_index(err, kv_len):
+    if err is not None and int(err.item()) != 0:
+        raise RuntimeError(f"sparse_attn: topk_idxs holds an index outside [-1, {kv_len})")
+
+
 def sparse_attn(q, kv, attn_sink, topk_idxs, scale):
     """
     Args:
@@ -87,21 +104,53 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, scale):
     Returns:
         o:          [b, m, h, d]   bf16, a new tensor on q's device
     """
-    if q.dim() != 4:
-        raise ValueError(f"q must be 4-D [b, m, h, d], got shape {tuple(q.shape)}")
-    if kv.dim() != 3 or attn_sink.dim() != 1 or topk_idxs.dim() != 3:
-        raise ValueError("expected kv [b, kv_len, d], attn_sink [h], topk_idxs [b, m, topk]")
-    if not (q.is_cuda and kv.is_cuda and attn_sink.is_cuda and topk_idxs.is_cuda):
-        raise ValueError("sparse_attn runs on the GPU only; move all inputs to the device")
-    load_extension()
-    # Same input handling as track-01/submission.py:995-998.
-    q_c = q.contiguous()
-    kv_c = kv.contiguous()
-    sink_c = attn_sink.contiguous()
-    idx_c = topk_idxs.contiguous()
+    q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
     err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
     o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags)
-    if err is not None and int(err.item()) != 0:
-        raise RuntimeError(
-            f"sparse_attn: topk_idxs holds an index outside [-1, {kv.shape[1]})")
+    _raise_if_bad_index(err, kv.shape[1])
     return o
+
+
+def sparse_attn_with_lse(q, kv, attn_sink, topk_idxs, scale):
+    """``sparse_attn`` that also returns the log-sum-exp of each (query, head).
+
+    Returns ``(o, lse)``: ``o`` as ``sparse_attn``; ``lse`` fp32 ``[b, m, h]``,
+    ``lse = ln(sum_t exp(s_t) + exp(attn_sink[h]))`` over the valid slots (the
+    ``m_total + ln(l_total)`` of track-01/submission.py:195-199), so that
+    ``o = sum_t exp(s_t - lse) * kv[idx_t]``. With ``attn_sink = -inf`` this is
+    a partial result for :func:`sparse_attn_merge`. A query with no mass at
+    all (no valid slot and sink = -inf) gets ``o = 0`` and ``lse = -inf``.
+    """
+    q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
+    err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
+    o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse(q_c, kv_c, sink_c, idx_c, float(scale),
+                                                  err, _flags)
+    _raise_if_bad_index(err, kv.shape[1])
+    return o, lse
+
+
+def sparse_attn_merge(o_parts, lse_parts, attn_sink=None):
+    """Merge partial results over disjoint slot subsets of the same queries.
+
+    Args:
+        o_parts:    [n, b, m, h, d] bf16 (a sequence of n [b, m, h, d] is stacked)
+        lse_parts:  [n, b, m, h]    fp32
+        attn_sink:  [h] fp32 or None (no sink)
+
+    Each part is :func:`sparse_attn_with_lse` over its slots with
+    ``attn_sink = -inf``; the merge folds the sink once:
+    ``lse = ln(sum_i exp(lse_i) + exp(sink))``, ``o = sum_i exp(lse_i - lse) o_i``,
+    which equals ``sparse_attn_with_lse`` over the union of the slots (the
+    sink algebra of track-01/notes.md:32-41). Returns ``(o, lse)``.
+    """
+    if isinstance(o_parts, (list, tuple)):
+        o_parts = torch.stack(list(o_parts))
+    if isinstance(lse_parts, (list, tuple)):
+        lse_parts = torch.stack(list(lse_parts))
+    if o_parts.dim() != 5 or lse_parts.dim() != 4:
+        raise ValueError("expected o_parts [n, b, m, h, d] and lse_parts [n, b, m, h]")
+    if not (o_parts.is_cuda and lse_parts.is_cuda and
+            (attn_sink is None or attn_sink.is_cuda)):
+        raise ValueError("sparse_attn_merge runs on the GPU only")
+    load_extension()
+    return torch.ops.sa_amd.sparse_attn_merge(o_parts, lse_parts, attn_sink)

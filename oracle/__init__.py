@@ -10,4 +10,7 @@ from .sparse_attn_ref import (  # noqa: F401
     sparse_attn_fp64,
     sparse_attn_bruteforce,
     masked_fold_fp64,
+    sparse_attn_lse_fp64,
+    merge_fp64,
+    sparse_attn_bruteforce_lse,
 )

@@ -31,6 +31,16 @@ Functions
 ``masked_fold_fp64``       float64 split-topk partials (running max, sum,
                            unnormalised output) merged with the sink folded in
                            last, the algebra of ``track-01/notes.md:32-41``.
+``sparse_attn_lse_fp64``   float64 ``(o, lse)``: ``lse = ln(sum_t exp(s_t) +
+                           exp(sink))``, the ``m_total + ln(l_total)`` of
+                           ``track-01/submission.py:195-199``.
+``merge_fp64``             float64 merge of partial ``(o_i, lse_i)`` over
+                           disjoint slot subsets with the sink folded once.
+``sparse_attn_bruteforce_lse``  scalar-loop ``lse`` (tiny shapes only).
+
+No-mass convention (outside the reference, whose softmax is 0/0 there): a
+query with no valid slot and ``sink = -inf`` gives ``o = 0`` and
+``lse = -inf``.
 
 Parity status: every function here is pinned by ``tests/test_oracle.py``
 (cross-checks between the three independent restatements, closed forms,
@@ -48,6 +58,9 @@ __all__ = [
     "sparse_attn_fp64",
     "sparse_attn_bruteforce",
     "masked_fold_fp64",
+    "sparse_attn_lse_fp64",
+    "merge_fp64",
+    "sparse_attn_bruteforce_lse",
     "check_indices",
 ]
 
@@ -241,4 +254,99 @@ def masked_fold_fp64(q, kv, attn_sink, topk_idxs, scale, nsplit: int) -> np.ndar
                          np.exp(np.where(np.isneginf(M), 0.0, M - m_tot)))
             l_tot = a * L + np.exp(sk - m_tot)
             out[bi, mi] = (a / l_tot)[:, None] * O
+    return out
+
+
+def sparse_attn_lse_fp64(q, kv, attn_sink, topk_idxs, scale):
+    """float64 ``(o, lse)`` per query on the compacted slots.
+
+    ``lse[b, m, h] = ln(sum_t exp(s_t) + exp(sink[h]))`` over the valid slots,
+    computed as ``zmax + ln(sum exp(z - zmax))`` with ``z`` the scores and the
+    sink; ``o`` is ``sparse_attn_fp64``'s. No mass (no slot, sink = -inf):
+    ``o = 0``, ``lse = -inf``. Returns float64 ``[b, m, h, d]`` and ``[b, m, h]``.
+    """
+    qn = _as_f64(q)
+    kvn = _as_f64(kv)
+    sk = _as_f64(attn_sink)
+    idx = np.asarray(topk_idxs.numpy() if isinstance(topk_idxs, torch.Tensor)
+                     else topk_idxs, dtype=np.int64)
+    b, m, h, d = qn.shape
+    kv_len = kvn.shape[1]
+    if ((idx < -1) | (idx >= kv_len)).any():
+        raise RuntimeError("sparse_attn: index out of bounds")
+    out = np.zeros((b, m, h, d), dtype=np.float64)
+    lse = np.full((b, m, h), -np.inf, dtype=np.float64)
+    for bi in range(b):
+        for mi in range(m):
+            rows = idx[bi, mi]
+            rows = rows[rows != -1]
+            K = kvn[bi, rows]                        # [n, d]
+            s = (qn[bi, mi] @ K.T) * float(scale)    # [h, n]
+            z = np.concatenate([s, sk[:, None]], axis=1)
+            zmax = z.max(axis=1)
+            live = ~np.isneginf(zmax)
+            zm = np.where(live, zmax, 0.0)
+            e = np.exp(z - zm[:, None])              # exp(-inf) = 0 for a -inf sink
+            den = e.sum(axis=1)
+            lse[bi, mi] = np.where(live, zm + np.log(np.where(live, den, 1.0)), -np.inf)
+            w = e[:, :-1] / np.where(live, den, 1.0)[:, None]
+            out[bi, mi] = np.where(live[:, None], w @ K, 0.0)
+    return out, lse
+
+
+def merge_fp64(o_parts, lse_parts, attn_sink=None):
+    """float64 merge of partials ``o_parts [n, b, m, h, d]``, ``lse_parts
+    [n, b, m, h]`` with the sink ``[h]`` (None: no sink) folded once:
+    ``lse = ln(sum_i exp(lse_i) + exp(sink))``, ``o = sum_i exp(lse_i - lse) o_i``.
+    A part with ``lse_i = -inf`` contributes nothing (its ``o_i`` is ignored).
+    Returns float64 ``[b, m, h, d]`` and ``[b, m, h]``."""
+    O = _as_f64(o_parts)
+    L = _as_f64(lse_parts)
+    n, b, m, h = L.shape
+    terms = list(L)
+    if attn_sink is not None:
+        terms.append(np.broadcast_to(_as_f64(attn_sink), (b, m, h)))
+    if not terms:
+        return np.zeros(O.shape[1:] if O.ndim == 5 else (b, m, h, 0)), np.full((b, m, h), -np.inf)
+    T = np.stack(terms)                              # [n(+1), b, m, h]
+    mx = T.max(axis=0)
+    live = ~np.isneginf(mx)
+    mz = np.where(live, mx, 0.0)
+    lse = np.where(live, mz + np.log(np.where(live, np.exp(T - mz).sum(axis=0), 1.0)),
+                   -np.inf)
+    out = np.zeros(O.shape[1:], dtype=np.float64)
+    for i in range(n):
+        li = L[i]
+        use = live & ~np.isneginf(li)
+        w = np.where(use, np.exp(np.where(use, li - np.where(live, lse, 0.0), 0.0)), 0.0)
+        out += np.where(use[..., None], w[..., None] * O[i], 0.0)
+    return out, lse
+
+
+def sparse_attn_bruteforce_lse(q, kv, attn_sink, topk_idxs, scale) -> np.ndarray:
+    """Scalar-loop ``lse[b, m, h] = ln(sum_t exp(s_t) + exp(sink[h]))`` with
+    ``math.log`` / ``math.exp`` over an explicit max (tiny shapes only)."""
+    qn = _as_f64(q).tolist()
+    kvn = _as_f64(kv).tolist()
+    sk = _as_f64(attn_sink).tolist()
+    idx = (topk_idxs.tolist() if isinstance(topk_idxs, torch.Tensor)
+           else np.asarray(topk_idxs).tolist())
+    b = len(qn)
+    m = len(qn[0]) if b else 0
+    h = len(qn[0][0]) if m else 0
+    d = len(qn[0][0][0]) if h else 0
+    out = np.full((b, m, h), -np.inf, dtype=np.float64)
+    for bi in range(b):
+        for mi in range(m):
+            rows = [r for r in idx[bi][mi] if r != -1]
+            for hi in range(h):
+                zs = []
+                for r in rows:
+                    zs.append(sum(qn[bi][mi][hi][di] * kvn[bi][r][di] for di in range(d))
+                              * float(scale))
+                zs.append(sk[hi])
+                mx = max(zs)
+                if mx == -math.inf:
+                    continue
+                out[bi, mi, hi] = mx + math.log(sum(math.exp(z - mx) for z in zs))
     return out

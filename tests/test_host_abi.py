@@ -31,7 +31,18 @@ class SaArgs(ctypes.Structure):
         ("sidx", ctypes.c_int64 * 3), ("so", ctypes.c_int64 * 4),
         ("scale", ctypes.c_float), ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t), ("err_word", ctypes.c_void_p),
-        ("flags", ctypes.c_uint32),
+        ("flags", ctypes.c_uint32), ("lse", ctypes.c_void_p), ("slse", ctypes.c_int64 * 3),
+    ]
+
+
+class SaMergeArgs(ctypes.Structure):
+    _fields_ = [
+        ("o_parts", ctypes.c_void_p), ("lse_parts", ctypes.c_void_p),
+        ("sink", ctypes.c_void_p), ("o", ctypes.c_void_p), ("lse", ctypes.c_void_p),
+        ("n", ctypes.c_int64), ("b", ctypes.c_int64), ("m", ctypes.c_int64),
+        ("h", ctypes.c_int64), ("d", ctypes.c_int64),
+        ("sop", ctypes.c_int64 * 5), ("slp", ctypes.c_int64 * 4),
+        ("so", ctypes.c_int64 * 4), ("slse", ctypes.c_int64 * 3),
     ]
 
 
@@ -56,6 +67,8 @@ def libs():
                                            ctypes.POINTER(ctypes.c_size_t)]
         lib.sa_strerror.restype = ctypes.c_char_p
     host.sa_host_validate.argtypes = [ctypes.POINTER(SaArgs)]
+    host.sa_host_validate_merge.argtypes = [ctypes.POINTER(SaMergeArgs)]
+    hip.sa_merge.argtypes = [ctypes.POINTER(SaMergeArgs), ctypes.c_void_p]
     host.sa_host_plan_full.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_int,
                                        ctypes.POINTER(ctypes.c_int64)]
     host.sa_host_plan.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_int,
@@ -84,7 +97,7 @@ def declared_functions():
 
 def test_header_declares_expected_api():
     assert declared_functions() == ["sa_abi_version", "sa_forward", "sa_forward_events",
-                                    "sa_strerror", "sa_workspace_bytes"]
+                                    "sa_merge", "sa_strerror", "sa_workspace_bytes"]
 
 
 def test_ctypes_binding_matches_header_layout():
@@ -93,9 +106,11 @@ def test_ctypes_binding_matches_header_layout():
     import sys
     sys.path.insert(0, PKG)
     import sa_capi
-    assert ctypes.sizeof(sa_capi.SaArgs) == ctypes.sizeof(SaArgs)
-    for (n1, _), (n2, _) in zip(sa_capi.SaArgs._fields_, SaArgs._fields_):
-        assert n1 == n2 and getattr(sa_capi.SaArgs, n1).offset == getattr(SaArgs, n2).offset
+    for mine, theirs in ((SaArgs, sa_capi.SaArgs), (SaMergeArgs, sa_capi.SaMergeArgs)):
+        assert ctypes.sizeof(theirs) == ctypes.sizeof(mine)
+        assert len(theirs._fields_) == len(mine._fields_)
+        for (n1, _), (n2, _) in zip(theirs._fields_, mine._fields_):
+            assert n1 == n2 and getattr(theirs, n1).offset == getattr(mine, n2).offset
     assert sa_capi.KERNELS == ("index", "order", "tile", "query", "combine")
     text = open(HEADER).read()
     assert "SA_KERNEL_COUNT = 5" in text
@@ -122,7 +137,7 @@ def test_library_exports_every_declared_symbol(libs):
     hip, _ = libs
     for name in declared_functions():
         assert hasattr(hip, name), f"{name} not exported"
-    assert hip.sa_abi_version() == 1
+    assert hip.sa_abi_version() == 2
 
 
 def test_strerror_covers_codes(libs):
@@ -273,3 +288,63 @@ def test_torch_operator_registers(libs):
     assert hasattr(torch.ops.sa_amd, "sparse_attn_fwd")
     schema = str(torch.ops.sa_amd.sparse_attn_fwd.default._schema)
     assert "Tensor q" in schema and "float scale" in schema
+
+
+def test_lse_argument_checks(libs):
+    hip, host = libs
+    a = good_args()
+    a.lse = 0x60002                      # not 4-byte aligned
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_EINVAL
+    a.lse = 0x60000
+    a.slse[:] = [64, 16, -1]
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_EINVAL
+    a.slse[:] = [64, 16, 1]
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_OK
+
+
+def good_merge(n=3, b=1, m=2, h=16, d=512):
+    a = SaMergeArgs()
+    a.o_parts, a.lse_parts, a.sink, a.o, a.lse = 0x10000, 0x20000, 0x30000, 0x40000, 0x50000
+    a.n, a.b, a.m, a.h, a.d = n, b, m, h, d
+    a.sop[:] = [b * m * h * d, m * h * d, h * d, d, 1]
+    a.slp[:] = [b * m * h, m * h, h, 1]
+    a.so[:] = [m * h * d, h * d, d, 1]
+    a.slse[:] = [m * h, h, 1]
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("n", -1, SA_EINVAL), ("d", 12, SA_EINVAL), ("o", 0, SA_EINVAL),
+    ("o_parts", 0, SA_EINVAL), ("lse_parts", 0, SA_EINVAL), ("o", 0x40008, SA_EINVAL),
+    ("lse", 0x50002, SA_EINVAL), ("sink", 0x30001, SA_EINVAL),
+])
+def test_merge_argument_errors(libs, field, value, code):
+    hip, host = libs
+    a = good_merge()
+    setattr(a, field, value)
+    assert host.sa_host_validate_merge(ctypes.byref(a)) == code
+    assert hip.sa_merge(ctypes.byref(a), None) == code
+
+
+@pytest.mark.parametrize("arr,i,value", [("sop", 4, 2), ("sop", 2, 7), ("so", 3, 2),
+                                         ("so", 1, -8), ("slp", 0, -1), ("slse", 2, -1)])
+def test_merge_stride_errors(libs, arr, i, value):
+    hip, host = libs
+    a = good_merge()
+    getattr(a, arr)[i] = value
+    assert host.sa_host_validate_merge(ctypes.byref(a)) == SA_EINVAL
+
+
+def test_merge_optional_and_empty(libs):
+    hip, host = libs
+    a = good_merge()
+    a.sink = None
+    a.lse = None
+    assert host.sa_host_validate_merge(ctypes.byref(a)) == SA_OK
+    a = good_merge(n=0)
+    a.o_parts = None                    # no parts: only o (and lse) are written
+    a.lse_parts = None
+    assert host.sa_host_validate_merge(ctypes.byref(a)) == SA_OK
+    a = good_merge(b=0)
+    a.o = None                          # empty output: nothing to check or run
+    assert hip.sa_merge(ctypes.byref(a), None) == SA_OK
