@@ -765,6 +765,19 @@ constexpr int kTilePitch = kRowBytes + 48;
 // gather's.
 constexpr int kPPitch = 2 * kTileRows + 16;  // bytes per P column line
 constexpr int kTileCols = kTQ * kHeads;      // 128 score columns
+#ifndef SA_K_RING
+#define SA_K_RING 6
+#endif
+#ifndef SA_DMA_EVERY
+#define SA_DMA_EVERY 4
+#endif
+// K fragments of S^T = K . Q^T in flight: each ds_read_b128 is issued
+// kKRing - 1 MFMAs before the MFMA that consumes it.
+constexpr int kKRing = SA_K_RING;
+// The 16 row gathers of a wave's share of the next step are issued one per
+// kDmaEvery MFMAs of S^T = K . Q^T.
+constexpr int kDmaEvery = SA_DMA_EVERY;
+static_assert(kDmaEvery * 16 <= 2 * (kDim / 16), "the gathers fit in the S^T MFMAs");
 
 __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kTilePitch];
@@ -881,27 +894,35 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   uint8_t* pwrite = s_p + (32 * wave + l32) * kPPitch + 8 * hi;
 
   // Softmax of one 32-row half of a step, cut into slots that ride between
-  // MFMAs: slots 0..7 turn two scores each into s * scale + log2 c (-inf for
-  // rows the query does not name) and take the column max, slot 8 merges the
-  // max of the lane pair and checks / sets the column's reference, slots
-  // 9..24 turn one score each into c * 2^(s - m) = 2^(x - m), add it to the
-  // column sum and store P as bf16 (every fourth slot). (v_dot2 forms of the
-  // sum stall the MFMAs they are interleaved with on gfx950: plain adds.)
-  constexpr int kSmSlots = 25;
+  // MFMAs. Each slot's instructions are independent of one another, so none
+  // of them waits on the previous one's result and holds up the next MFMA:
+  //  * slots 0..7 turn two scores each into x = s * scale + log2 c (-inf for
+  //    rows the query does not name); slots 1..8 fold the previous slot's two
+  //    into the column max;
+  //  * slot 9 merges the max of the lane pair, slot 10 checks / sets the
+  //    column's reference;
+  //  * element e is shifted (x - m) in slot 11 + e, exponentiated in slot
+  //    12 + e and added to the column sum / packed to bf16 in slot 13 + e;
+  //    P is stored every fourth element.
+  // (v_dot2 forms of the sum stall the MFMAs they are interleaved with on
+  // gfx950: plain adds.)
+  constexpr int kSmSlots = 29;
   bool abort_any = false;  // wave-uniform: a column jumped above its reference
   auto sm_slot = [&](int k, f32x16& x, const f16x4(&lc)[4], int rb, float& mx, float& mref,
                      float& psum, bf16x4& pk) {
+    if (k >= 1 && k <= 8)
+      mx = fmaxf(mx, fmaxf(x[2 * k - 2], x[2 * k - 1]));  // v_max3
     if (k < 8) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const int e = 2 * k + t;
         x[e] = fmaf(x[e], p.scale_log2, static_cast<float>(lc[e >> 2][e & 3]));
-        mx = fmaxf(mx, x[e]);
       }
-    } else if (k == 8) {
+    } else if (k == 9) {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
                                                        false, false);
       mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));  // -inf: no row in the half
+    } else if (k == 10) {
       // Fixed reference: a column keeps the max of its first non-empty half.
       // A later score more than kTileMaxJump above it would need O rescaled;
       // the tile then hands itself to the per-query kernel.
@@ -909,14 +930,20 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       if (m_run == -INFINITY) m_run = mx;
       mref = m_run == -INFINITY ? 0.f : m_run;  // column still empty
     } else if (k < kSmSlots) {
-      const int e = k - 9;
-      const float pj = __builtin_amdgcn_exp2f(x[e] - mref);  // c * 2^(s - m); 0 if masked
-      psum += pj;
-      asm volatile("" : "+v"(psum));  // keep the sum in its slot (not sunk to the loop end)
-      pk[e & 3] = static_cast<__bf16>(pj);
-      if ((e & 3) == 3) *reinterpret_cast<bf16x4*>(pwrite + 2 * (32 * rb + 8 * (e >> 2))) = pk;
+      const int c = k - 13;  // sum and pack
+      if (c >= 0 && c < 16) {
+        psum += x[c];
+        asm volatile("" : "+v"(psum));  // keep the sum in its slot (not sunk to the loop end)
+        pk[c & 3] = static_cast<__bf16>(x[c]);
+        if ((c & 3) == 3) *reinterpret_cast<bf16x4*>(pwrite + 2 * (32 * rb + 8 * (c >> 2))) = pk;
+      }
+      const int b = k - 12;  // c * 2^(s - m); 0 if masked
+      if (b >= 0 && b < 16) x[b] = __builtin_amdgcn_exp2f(x[b]);
+      const int a = k - 11;
+      if (a >= 0 && a < 16) x[a] -= mref;
     }
   };
+  static_assert(kSmSlots <= 32, "the softmax of a half fits in 32 MFMA slots");
 
   for (int step = 0; step < nsteps; ++step) {
     const int buf = step & 1;
@@ -945,22 +972,23 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     }
     {
       const uint8_t* kr = tb + koff;
-      bf16x8 kf[3];
+      bf16x8 kf[kKRing];
       auto kread = [&](int i, int slot) {
         kf[slot] = *reinterpret_cast<const bf16x8*>(kr + (i >> 5) * 32 * kTilePitch + 32 * (i & 31));
       };
-      kread(0, 0);
-      kread(1, 1);
+#pragma unroll
+      for (int i = 0; i < kKRing - 1; ++i) kread(i, i);
       float mx = -INFINITY, mref = 0.f, psum = 0.f;
       bf16x4 pk;
 #pragma unroll
       for (int i = 0; i < 2 * (kDim / 16); ++i) {
-        if (i + 2 < 2 * (kDim / 16)) kread(i + 2, (i + 2) % 3);
+        if (i + kKRing - 1 < 2 * (kDim / 16)) kread(i + kKRing - 1, (i + kKRing - 1) % kKRing);
         if (i < kDim / 16)
-          sacc0 = mfma_32x32x16(kf[i % 3], qf[i], sacc0);
+          sacc0 = mfma_32x32x16(kf[i % kKRing], qf[i], sacc0);
         else
-          sacc1 = mfma_32x32x16(kf[i % 3], qf[i - kDim / 16], sacc1);
-        if (i < kDim / 16 && (i & 1) == 1) dma_row(rows_next, i >> 1, buf ^ 1);
+          sacc1 = mfma_32x32x16(kf[i % kKRing], qf[i - kDim / 16], sacc1);
+        if (i % kDmaEvery == kDmaEvery - 1 && i / kDmaEvery < kRowsPerWave)
+          dma_row(rows_next, i / kDmaEvery, buf ^ 1);
         if (i == 1) dma_counts(nxt, buf ^ 1);
         if (i >= kDim / 16) sm_slot(i - kDim / 16, sacc0, lc0, 0, mx, mref, psum, pk);
         __builtin_amdgcn_sched_barrier(0);  // keep the interleave
