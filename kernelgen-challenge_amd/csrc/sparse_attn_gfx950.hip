@@ -104,8 +104,10 @@ struct FwdParams {
   __bf16* o;
   float* part;          // [units * nsplit] x (ml[32] + O[16*512]) when split
   int32_t* err;
-  const int32_t* tile_meta;  // non-null: skip queries of shared tiles
-  int64_t tiles_per_b;
+  // Non-null with a shared-row plan: pq[0] is the number of queries left to
+  // this kernel and pq[1..] their flat ids b * m + m_i; the grid strides over
+  // them. Null: work-group i runs unit i (query i / nsplit, part i % nsplit).
+  const int32_t* pq;
   int64_t m, kv_len, topk;
   int64_t sq_b, sq_m, sq_h;
   int64_t skv_b, skv_n;
@@ -130,6 +132,7 @@ struct IndexParams {
   int64_t skv_n;        // kv row stride (elements)
   int64_t tiles_per_b, cap;
   int force;            // shared mode whenever the counts fit
+  int vec4;             // indices readable as int4 (aligned base, strides and topk)
 };
 
 struct TileParams {
@@ -139,6 +142,7 @@ struct TileParams {
   __bf16* o;
   const int32_t* meta;
   int32_t* meta_out;    // same array: a tile that must rescale marks itself per-query
+  int32_t* pq;          // ... and appends its queries to the per-query work list
   const int32_t* order; // work-group i runs tile order[i]
   const uint32_t* row_off;
   const _Float16* lcnt;
@@ -309,12 +313,24 @@ __device__ __forceinline__ float wave_sum16(float x) {
 // ============================================================================
 // per-query kernel
 // ============================================================================
-__global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kRowStride];
-  __shared__ __attribute__((aligned(16))) int32_t s_list[kListCap];
-  __shared__ __attribute__((aligned(16))) __bf16 s_p[kHeads * kTileRows];
-  __shared__ float s_red[kWaves][kHeads];
-  __shared__ int s_cnt[kWaves];
+struct QuerySmem {
+  uint8_t tile[2][kTileRows * kRowStride];
+  int32_t list[kListCap];
+  __bf16 p[kHeads * kTileRows];
+  float red[kWaves][kHeads];
+  int cnt[kWaves];
+};
+
+// One (query, topk part) unit of the per-query kernel. Leaves every wave past
+// its last LDS access of `sm` only after the work-group's final barrier, so a
+// following unit may reuse `sm` after one more __syncthreads().
+__device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t unit,
+                                           QuerySmem& sm) {
+  auto& s_tile = sm.tile;
+  auto& s_list = sm.list;
+  auto& s_p = sm.p;
+  auto& s_red = sm.red;
+  auto& s_cnt = sm.cnt;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -322,14 +338,10 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdPara
   const int n = lane & 15;   // MFMA column lane: head (S^T, P) or d (O)
   const int g = lane >> 4;   // MFMA k-group
 
-  const int64_t unit = blockIdx.x;
   const int64_t qid = unit / p.nsplit;
   const int split = int(unit % p.nsplit);
   const int64_t bi = qid / p.m;
   const int64_t mi = qid % p.m;
-  if (p.tile_meta != nullptr &&
-      p.tile_meta[(bi * p.tiles_per_b + mi / kTQ) * kMetaInts + 1] == kModeShared)
-    return;  // this query belongs to a shared-row tile
   const int64_t s_begin = int64_t(split) * p.split_len;
   const int64_t s_end = min(p.topk, s_begin + p.split_len);
 
@@ -530,6 +542,22 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdPara
   }
 }
 
+// kListed = false: work-group i runs unit i. kListed = true (shared-row
+// plans): the grid strides over the work list p.pq.
+template <bool kListed>
+__global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdParams p) {
+  __shared__ __attribute__((aligned(16))) QuerySmem sm;
+  if constexpr (!kListed) {
+    query_unit(p, blockIdx.x, sm);
+  } else {
+    const int nu = __builtin_amdgcn_readfirstlane(p.pq[0]);
+    for (int k = blockIdx.x; k < nu; k += gridDim.x) {
+      query_unit(p, p.pq[1 + k], sm);
+      __syncthreads();  // every wave is done with sm before the next unit
+    }
+  }
+}
+
 // ============================================================================
 // tile index kernel
 // ============================================================================
@@ -542,14 +570,31 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdPara
 // the row, so that s * scale + value is the masked, multiplicity-weighted
 // score in the log2 domain. A lane reads 4 consecutive rows of its query as
 // 8 bytes.
-constexpr int kIdxBatch = 8;                       // index loads per thread per batch
-constexpr int kIdxBatchSlots = kIdxBatch * kThreads;
+// One work-group of kIdxThreads per tile. Three phases, each with many
+// independent memory operations in flight per wave:
+//  1. count: the tile's indices are read as int4 (int32 when the index rows
+//     are not 16-byte aligned), kIdxVec per thread per round, all of a round
+//     issued before any is used; every valid index is added to the u64 LDS
+//     counter of its row (byte q = count in tile query q), and the valid
+//     slots are counted with ballots.
+//  2. scan: wave w takes a contiguous run of 64-row chunks and counts its
+//     nonzero rows, its first row and the sum of all count bytes, reading
+//     kIdxScan chunks per batch. A count passing 255 carries into the next
+//     byte (or out of the word) and lowers that sum, so a sum below the
+//     valid slots makes the tile per-query.
+//  3. write: the waves' run lengths give each its first union entry; a
+//     ballot per chunk ranks the nonzero rows, so the union is written in
+//     ascending row order with consecutive lanes on consecutive entries.
+constexpr int kIdxThreads = 512;
+constexpr int kIdxWaves = kIdxThreads / 64;
+constexpr int kIdxVec = 4;    // index vectors per thread per round
+constexpr int kIdxScan = 4;   // LDS chunk reads per wave per batch
 
-__global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexParams p) {
+__global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexParams p) {
   extern __shared__ unsigned long long s_count[];  // [kv_len], byte q = count in query q
-  __shared__ int s_wtot[kWaves];
-  __shared__ int s_nv[kTQ];
-  __shared__ int s_bsum[kTQ];
+  __shared__ int s_wtot[kIdxWaves];
+  __shared__ int s_nvalid;   // valid slots of the tile
+  __shared__ int s_bytes;    // sum of every count byte
   __shared__ int s_first;
 
   const int tid = threadIdx.x;
@@ -560,90 +605,104 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
   const int64_t q0 = (tile % p.tiles_per_b) * kTQ;
   const int qt = int(min(int64_t(kTQ), p.m - q0));
   const int kvl = int(p.kv_len);
+  const int topk = int(p.topk);
 
-  for (int i = tid; i < kvl; i += kThreads) s_count[i] = 0ull;
-  if (tid < kTQ) {
-    s_nv[tid] = 0;
-    s_bsum[tid] = 0;
+  for (int i = tid; i < kvl; i += kIdxThreads) s_count[i] = 0ull;
+  if (tid == 0) {
+    s_first = kvl;
+    s_nvalid = 0;
+    s_bytes = 0;
   }
-  if (tid == 0) s_first = kvl;
   __syncthreads();
 
-  // ---- multiplicity table. The slots are read in batches of kIdxBatchSlots
-  // of one query; the next batch's loads are in flight while this one is
-  // counted, so a tile costs about one memory latency per batch.
-  const int64_t nbq = (p.topk + kIdxBatchSlots - 1) / kIdxBatchSlots;  // batches per query
-  const int64_t nbt = nbq * qt;
+  // ---- 1. count --------------------------------------------------------------
   const int32_t* ib = p.idx + bi * p.si_b + q0 * p.si_m;
-  auto load = [&](int64_t k, int (&v)[kIdxBatch]) {
-    const int64_t qq = k / nbq;
-    const int64_t t0 = (k - qq * nbq) * kIdxBatchSlots + tid;
-    const int32_t* irow = ib + qq * p.si_m;
-#pragma unroll
-    for (int u = 0; u < kIdxBatch; ++u) {
-      const int64_t t = t0 + u * kThreads;
-      v[u] = t < p.topk ? irow[t] : -1;  // past the end: skipped like a -1 slot
-    }
+  bool bad = false;  // an index outside [-1, kv_len)
+  int nvalid = 0;    // wave-uniform
+  auto count = [&](int v, int qq) {
+    const bool ok = v >= 0 && v < kvl;
+    if (ok) atomicAdd(&s_count[v], 1ull << (8 * qq));
+    bad = bad || (!ok && v != -1);
+    nvalid += __popcll(__ballot(ok));
   };
-  bool bad = false;
-  int va[kIdxBatch], vb[kIdxBatch];
+  if (p.vec4) {  // topk, the row strides and the base are multiples of 4 int32
+    const int rv = topk / 4;          // int4 per query row
+    const int nv = qt * rv;
+    for (int e0 = 0; e0 < nv; e0 += kIdxThreads * kIdxVec) {
+      int4 v[kIdxVec];
+      int qv[kIdxVec];
 #pragma unroll
-  for (int u = 0; u < kIdxBatch; ++u) va[u] = vb[u] = -1;
-  if (nbt > 0) load(0, va);
-  for (int64_t k = 0; k < nbt; ++k) {
-    if (k + 1 < nbt) load(k + 1, vb);
-    const int qq = int(k / nbq);
-    const unsigned long long one = 1ull << (8 * qq);
-    int nv = 0;  // wave-uniform
+      for (int u = 0; u < kIdxVec; ++u) {
+        const int e = e0 + u * kIdxThreads + tid;
+        const int qq = e / max(rv, 1);
+        qv[u] = qq;
+        v[u] = e < nv ? *reinterpret_cast<const int4*>(ib + qq * p.si_m + 4 * (e - qq * rv))
+                      : int4{-1, -1, -1, -1};
+      }
 #pragma unroll
-    for (int u = 0; u < kIdxBatch; ++u) {
-      const int v = va[u];
-      const bool ok = v >= 0 && v < kvl;
-      if (ok) atomicAdd(&s_count[v], one);
-      bad |= !ok && v != -1;
-      nv += __popcll(__ballot(ok));
+      for (int u = 0; u < kIdxVec; ++u) {
+        count(v[u].x, qv[u]);
+        count(v[u].y, qv[u]);
+        count(v[u].z, qv[u]);
+        count(v[u].w, qv[u]);
+      }
     }
-    if (lane == 0 && nv != 0) atomicAdd(&s_nv[qq], nv);
+  } else {
+    const int nv = qt * topk;
+    for (int e0 = 0; e0 < nv; e0 += kIdxThreads * kIdxVec * 4) {
+      int v[4 * kIdxVec];
+      int qv[4 * kIdxVec];
 #pragma unroll
-    for (int u = 0; u < kIdxBatch; ++u) va[u] = vb[u];
+      for (int u = 0; u < 4 * kIdxVec; ++u) {
+        const int e = e0 + u * kIdxThreads + tid;
+        const int qq = e / max(topk, 1);
+        qv[u] = qq;
+        v[u] = e < nv ? ib[qq * p.si_m + (e - qq * topk)] : -1;
+      }
+#pragma unroll
+      for (int u = 0; u < 4 * kIdxVec; ++u) count(v[u], qv[u]);
+    }
   }
   if (bad && p.err != nullptr) atomicOr(p.err, 1);
+  if (lane == 0 && nvalid != 0) atomicAdd(&s_nvalid, nvalid);
   __syncthreads();
 
-  // ---- ascending union. Wave w scans a contiguous run of 64-row chunks; a
-  // ballot per chunk ranks its nonzero rows, so each wave writes its part of
-  // the union with consecutive lanes on consecutive entries.
+  // ---- 2. scan -----------------------------------------------------------------
   const int nchunks = (kvl + 63) / 64;
-  const int cpw = (nchunks + kWaves - 1) / kWaves;
+  const int cpw = (nchunks + kIdxWaves - 1) / kIdxWaves;
   const int c_lo = min(nchunks, wave * cpw);
   const int c_hi = min(nchunks, c_lo + cpw);
   int wcount = 0;  // wave-uniform
   int wfirst = kvl;
-  int bsum[kTQ];
+  int bytes = 0;   // this lane's sum of count bytes
+  for (int c0 = c_lo; c0 < c_hi; c0 += kIdxScan) {
+    unsigned long long wv[kIdxScan];
 #pragma unroll
-  for (int k = 0; k < kTQ; ++k) bsum[k] = 0;
-  for (int c = c_lo; c < c_hi; ++c) {
-    const int i = c * 64 + lane;
-    const unsigned long long w = i < kvl ? s_count[i] : 0ull;
-    const unsigned long long bm = __ballot(w != 0ull);
-    if (bm != 0ull && wfirst == kvl) wfirst = c * 64 + __ffsll((long long)bm) - 1;
-    wcount += __popcll(bm);
+    for (int u = 0; u < kIdxScan; ++u) {
+      const int i = (c0 + u) * 64 + lane;
+      wv[u] = (c0 + u < c_hi && i < kvl) ? s_count[i] : 0ull;
+    }
 #pragma unroll
-    for (int k = 0; k < kTQ; ++k) bsum[k] += int((w >> (8 * k)) & 255ull);
+    for (int u = 0; u < kIdxScan; ++u) {
+      const unsigned long long bm = __ballot(wv[u] != 0ull);
+      if (bm != 0ull && wfirst == kvl) wfirst = (c0 + u) * 64 + __ffsll((long long)bm) - 1;
+      wcount += __popcll(bm);
+      // the 8 bytes as four 16-bit pair sums, then their total
+      const unsigned long long pairs =
+          (wv[u] & 0x00FF00FF00FF00FFull) + ((wv[u] >> 8) & 0x00FF00FF00FF00FFull);
+      bytes += int((pairs * 0x0001000100010001ull) >> 48);
+    }
   }
   if (lane == 0) s_wtot[wave] = wcount;
-#pragma unroll
-  for (int k = 0; k < kTQ; ++k) {
-    int v = bsum[k];
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    if (lane == 0 && v != 0) atomicAdd(&s_bsum[k], v);
-  }
+  for (int off = 32; off > 0; off >>= 1) bytes += __shfl_xor(bytes, off);
+  if (lane == 0 && bytes != 0) atomicAdd(&s_bytes, bytes);
   if (lane == 0 && wfirst < kvl) atomicMin(&s_first, wfirst);
   __syncthreads();
+
+  // ---- 3. write ------------------------------------------------------------------
   int pos = 0;
   int nU = 0;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) {
+  for (int w = 0; w < kIdxWaves; ++w) {
     const int t = s_wtot[w];
     pos += (w < wave) ? t : 0;
     nU += t;
@@ -657,28 +716,34 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
 #pragma unroll
     for (int k = 0; k < kTQ; ++k) {
       const unsigned c = unsigned((w >> (8 * k)) & 255ull);
-      cb[k * kTileRows] = c == 0u ? static_cast<_Float16>(-INFINITY)
-                                  : static_cast<_Float16>(log2f(float(c)));
+      // v_log_f32 is log2; its error on 2..255 is far below fp16's half ulp
+      // at the rounding (exact at powers of two after it)
+      cb[k * kTileRows] = c == 0u   ? static_cast<_Float16>(-INFINITY)
+                          : c == 1u ? static_cast<_Float16>(0.f)
+                                    : static_cast<_Float16>(__builtin_amdgcn_logf(float(c)));
     }
   };
   const unsigned long long below = (1ull << lane) - 1ull;  // lanes under this one
-  for (int c = c_lo; c < c_hi; ++c) {
-    const int i = c * 64 + lane;
-    const unsigned long long w = i < kvl ? s_count[i] : 0ull;
-    const unsigned long long bm = __ballot(w != 0ull);
-    if (w != 0ull) put(pos + __popcll(bm & below), i, w);
-    pos += __popcll(bm);
+  for (int c0 = c_lo; c0 < c_hi; c0 += kIdxScan) {
+    unsigned long long wv[kIdxScan];
+#pragma unroll
+    for (int u = 0; u < kIdxScan; ++u) {
+      const int i = (c0 + u) * 64 + lane;
+      wv[u] = (c0 + u < c_hi && i < kvl) ? s_count[i] : 0ull;
+    }
+#pragma unroll
+    for (int u = 0; u < kIdxScan; ++u) {
+      const unsigned long long bm = __ballot(wv[u] != 0ull);
+      if (wv[u] != 0ull) put(pos + __popcll(bm & below), (c0 + u) * 64 + lane, wv[u]);
+      pos += __popcll(bm);
+    }
   }
   // pad to whole 64-row steps with a valid row of count 0
   const int padded = (nU + kTileRows - 1) / kTileRows * kTileRows;
-  for (int e = nU + tid; e < padded; e += kThreads) put(e, s_first, 0ull);
+  for (int e = nU + tid; e < padded; e += kIdxThreads) put(e, s_first, 0ull);
   if (tid == 0) {
-    bool overflow = false;
-    int total = 0;
-    for (int k = 0; k < kTQ; ++k) {
-      overflow |= s_bsum[k] != s_nv[k];  // a count passed 255 and carried
-      total += s_nv[k];
-    }
+    const int total = s_nvalid;
+    const bool overflow = s_bytes != total;  // a count carried
     // shared when the dense (query x union row) work is at most
     // kSharedWaste times the valid slots
     const bool shared =
@@ -699,23 +764,46 @@ __global__ void __launch_bounds__(kThreads) sa_tile_index_kernel(const IndexPara
 // kernel's work-group i runs tile order[i]; work-groups start in index order,
 // so the longest tiles start first and the short ones fill in at the end.
 // Tiles with equal keys may come in any order: each tile is independent.
+// The queries of per-query tiles go to the per-query kernel's work list
+// (pq[0] = count, pq[1..] = flat query ids), in any order.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderKeys = int(sa::kMaxTileKv / kTileRows) + 1;
 constexpr int kOrderKeysPadded = (kOrderKeys + 63) / 64 * 64;
 
-__global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const int32_t* meta,
-                                                                      int32_t* order,
-                                                                      int ntiles) {
+struct OrderParams {
+  const int32_t* meta;
+  int32_t* order;
+  int32_t* pq;
+  int ntiles;
+  int64_t m, tiles_per_b;
+};
+
+__global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const OrderParams p) {
   __shared__ int s_pos[kOrderKeysPadded];
+  __shared__ int s_npq;
   const int tid = threadIdx.x;
+  const int32_t* meta = p.meta;
+  const int ntiles = p.ntiles;
   for (int i = tid; i < kOrderKeysPadded; i += kOrderThreads) s_pos[i] = 0;
+  if (tid == 0) s_npq = 0;
   __syncthreads();
   auto key = [&](int t) {
     const int32_t* mt = meta + int64_t(t) * kMetaInts;
     return mt[1] == kModeShared ? (mt[0] + kTileRows - 1) / kTileRows : 0;
   };
-  for (int t = tid; t < ntiles; t += kOrderThreads) atomicAdd(&s_pos[key(t)], 1);
+  for (int t = tid; t < ntiles; t += kOrderThreads) {
+    const int k = key(t);
+    atomicAdd(&s_pos[k], 1);
+    if (meta[int64_t(t) * kMetaInts + 1] != kModeShared) {
+      const int64_t bi = t / p.tiles_per_b;
+      const int64_t q0 = (t % p.tiles_per_b) * kTQ;
+      const int qt = int(min(int64_t(kTQ), p.m - q0));
+      const int pos = atomicAdd(&s_npq, qt);
+      for (int j = 0; j < qt; ++j) p.pq[1 + pos + j] = int32_t(bi * p.m + q0 + j);
+    }
+  }
   __syncthreads();
+  if (tid == 0) p.pq[0] = s_npq;
   if (tid < 64) {
     // exclusive scan over descending keys: the start of key k is the number
     // of tiles with a larger key
@@ -734,7 +822,7 @@ __global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const int3
     }
   }
   __syncthreads();
-  for (int t = tid; t < ntiles; t += kOrderThreads) order[atomicAdd(&s_pos[key(t)], 1)] = t;
+  for (int t = tid; t < ntiles; t += kOrderThreads) p.order[atomicAdd(&s_pos[key(t)], 1)] = t;
 }
 
 // ============================================================================
@@ -1061,7 +1149,11 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 
     dma_barrier();  // every wave's prefetch has landed; P and this tile are free
     if (abort_seen != 0) {  // uniform: every wave read it after the same barrier
-      if (tid == 0) p.meta_out[tile * kMetaInts + 1] = sa::kModePerQuery;
+      if (tid == 0) {       // the per-query kernel, launched next, takes the tile's queries
+        p.meta_out[tile * kMetaInts + 1] = sa::kModePerQuery;
+        const int pos = atomicAdd(p.pq, qt);
+        for (int j = 0; j < qt; ++j) p.pq[1 + pos + j] = int32_t(bi * p.m + q0 + j);
+      }
       return;               // no o written; no transfer in flight
     }
   }
@@ -1367,20 +1459,29 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     ip.tiles_per_b = plan.tiles_per_b;
     ip.cap = plan.tile_cap;
     ip.force = (a->flags & SA_FLAG_FORCE_TILES) ? 1 : 0;
+    ip.vec4 = ((reinterpret_cast<uintptr_t>(a->idx) & 15u) == 0 && a->topk % 4 == 0 &&
+               a->sidx[0] % 4 == 0 && a->sidx[1] % 4 == 0) ? 1 : 0;
     const size_t lds = size_t(a->kv_len) * sizeof(unsigned long long);
     if (lds > 65536 &&
         hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
       return SA_EHIP;
     if (!mark(SA_KERNEL_INDEX, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), lds,
+    hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kIdxThreads), lds,
                        stream, ip);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
     if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
     int32_t* order = reinterpret_cast<int32_t*>(ws + plan.order_off);
     if (!mark(SA_KERNEL_ORDER, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream,
-                       static_cast<const int32_t*>(ip.meta), order, int(plan.ntiles));
+    int32_t* pq = reinterpret_cast<int32_t*>(ws + plan.pq_off);
+    OrderParams op{};
+    op.meta = ip.meta;
+    op.order = order;
+    op.pq = pq;
+    op.ntiles = int(plan.ntiles);
+    op.m = a->m;
+    op.tiles_per_b = plan.tiles_per_b;
+    hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, op);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
     if (!mark(SA_KERNEL_ORDER, 1)) return SA_EHIP;
 
@@ -1391,6 +1492,7 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.o = p.o;
     tp.meta = ip.meta;
     tp.meta_out = ip.meta;
+    tp.pq = pq;
     tp.order = order;
     tp.row_off = ip.row_off;
     tp.lcnt = ip.lcnt;
@@ -1416,13 +1518,19 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
                        stream, tp);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
     if (!mark(SA_KERNEL_TILE, 1)) return SA_EHIP;
-    p.tile_meta = ip.meta;
-    p.tiles_per_b = plan.tiles_per_b;
+    // the per-query kernel strides over the work list with one work-group
+    // per compute unit (its LDS allows one per CU)
+    p.pq = pq;
+    p.nblocks = min(p.nblocks, int64_t(cus));
   }
 
   if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
-  hipLaunchKernelGGL(sa_fwd_query_kernel, dim3(unsigned(p.nblocks)), dim3(kThreads), 0, stream,
-                     p);
+  if (p.pq != nullptr)
+    hipLaunchKernelGGL(sa_fwd_query_kernel<true>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL(sa_fwd_query_kernel<false>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
+                       stream, p);
   if (hipGetLastError() != hipSuccess) return SA_EHIP;
   if (!mark(SA_KERNEL_QUERY, 1)) return SA_EHIP;
   if (plan.nsplit > 1) {

@@ -167,3 +167,49 @@ def test_tiles_deterministic(gpu_sa):
     a = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
     b = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
     assert torch.equal(a, b)
+
+
+def test_per_query_work_list_matches_direct_launch(gpu_sa):
+    """A tile plan whose tiles all go to the per-query kernel (low overlap):
+    the kernel strides over the work list the order kernel writes, one
+    work-group per CU, several queries per work-group (300 > 256 CUs), a
+    ragged last tile. Each query must equal the direct per-query launch
+    bit for bit, and the sampled oracle check must pass."""
+    q, kv, sink, idx, sc = rand_case(1, 300, 16384, 256, seed=21, minus1=0.1)
+    o_l = run(q, kv, sink, idx, sc)
+    o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY)
+    assert torch.equal(o_l, o_p)
+    sampled_check(o_l, q, kv, sink, idx, sc, [(0, t) for t in (0, 1, 150, 295, 296, 299)],
+                  "work list")
+
+
+def test_work_list_mixed_with_aborted_tile(gpu_sa):
+    """Shared tiles, per-query tiles from the index kernel and a tile that
+    aborts at run time (scores jump far above its reference) in one call: the
+    aborted tile's queries are appended to the work list by the tile kernel
+    and computed by the per-query kernel launched next."""
+    # 256 queries (as many as CUs, so the plan does not split them)
+    q, kv, sink, idx, sc = rand_case(1, 256, 2048, 512, seed=22)
+    # queries 0..31: overlapping windows (shared tiles); 32..255 stay random
+    # (per-query tiles from the index kernel)
+    for t in range(32):
+        idx[0, t] = torch.arange(512, dtype=torch.int32) + 4 * t
+    # tile 1 (queries 8..15): a last row whose score for query 8 is far above
+    # everything the tile's first step sees
+    idx[0, 8:16, -1] = 2000
+    kv[0, 2000] = (q[0, 8].float().mean(0) * 60).to(torch.bfloat16)
+    o = run(q, kv, sink, idx, sc).cpu()
+    o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY).cpu()
+    d = (o.float() - o_p.float()).abs()
+    say(f"  mixed list: max {d.max().item():.3e}")
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
+    assert torch.equal(o[0, 8:16], o_p[0, 8:16])   # the aborted tile ran per query
+    assert torch.equal(o[0, 32:], o_p[0, 32:])     # per-query tiles
+    sampled_check(o, q, kv, sink, idx, sc, [(0, t) for t in (0, 7, 16, 31, 40, 255)], "mixed")
+    # row 2000 dominates queries 8..15 (|o| up to ~20, bf16 ulp 0.125 there):
+    # relative RMS against float64 instead of the absolute bound
+    exp = sparse_attn_fp64(q[:, 8:16], kv, sink, idx[:, 8:16], sc)
+    err = o[:, 8:16].double().numpy() - exp
+    rel = float(np.sqrt((err ** 2).mean() / (exp ** 2).mean()))
+    say(f"  aborted tile: rel_rms={rel:.3e}")
+    assert rel <= 5e-3

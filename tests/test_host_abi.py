@@ -215,9 +215,10 @@ PART_BYTES = 2 * 16 * 4 + 16 * 512 * 4
 
 
 def plan_full(host, a, cus):
-    out = (ctypes.c_int64 * 7)()
+    out = (ctypes.c_int64 * 13)()
     assert host.sa_host_plan_full(ctypes.byref(a), cus, out) == SA_OK
-    keys = ["nsplit", "split_len", "tiles", "tiles_per_b", "ntiles", "tile_cap", "ws"]
+    keys = ["nsplit", "split_len", "tiles", "tiles_per_b", "ntiles", "tile_cap", "ws",
+            "meta_off", "order_off", "rows_off", "cnts_off", "pq_off", "part_off"]
     return dict(zip(keys, list(out)))
 
 
@@ -244,8 +245,16 @@ def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
         assert p["tiles_per_b"] == -(-m // 8) and p["ntiles"] == b * p["tiles_per_b"]
         assert p["tile_cap"] % 64 == 0 and p["tile_cap"] >= min(kv_len, 8 * topk)
         # per tile: meta, its slot in the launch order, a 32-bit offset per
-        # union row and an fp16 log2 multiplicity per (query, union row)
-        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 2 * 8) * p["tile_cap"])
+        # union row and an fp16 log2 multiplicity per (query, union row); then
+        # the per-query work list (a count and up to b * m query ids)
+        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 2 * 8) * p["tile_cap"]) + 4 * (1 + b * m)
+        regions = [(p["meta_off"], 16 * p["ntiles"]), (p["order_off"], 4 * p["ntiles"]),
+                   (p["rows_off"], 4 * p["ntiles"] * p["tile_cap"]),
+                   (p["cnts_off"], 2 * 8 * p["ntiles"] * p["tile_cap"]),
+                   (p["pq_off"], 4 * (1 + b * m))]
+        for (o0, n0), (o1, _) in zip(regions, regions[1:]):
+            assert o0 % 256 == 0 and o0 + n0 <= o1           # aligned, disjoint, in order
+        assert regions[-1][0] + regions[-1][1] <= p["ws"]
 
 
 @pytest.mark.parametrize("b,m,topk,cus,expect_ns,expect_len", [
