@@ -18,7 +18,7 @@
 //   batch: counts every valid index of the tile's queries in an LDS table
 //   (one byte per query), writes the row union in ascending order (32-bit
 //   byte offsets) with an fp16 log2 multiplicity per (query, row), and marks
-//   the tile "shared" when the dense (query x union row) work is at most 3x
+//   the tile "shared" when the dense (query x union row) work is at most 4x
 //   its valid slots, else "per query".
 // sa_tile_order_kernel  one work-group: counting sort of the tiles by
 //   descending step count, so the longest tiles are launched first.
@@ -79,9 +79,11 @@ constexpr float kTileMaxJump = 24.f;
 
 constexpr int kTQ = sa::kTileQueries;       // queries per shared tile
 // A tile is shared when the dense (query x union row) MFMA work is at most
-// this multiple of its valid (query, slot) pairs: gathering every query's rows
-// separately costs about as much per pair as several dense MFMA pairs.
-constexpr int kSharedWaste = 3;
+// this multiple of its valid (query, slot) pairs. Measured on MI355X, the
+// shared-row kernel spends about 6.6 ns of one CU per dense (query, row) pair
+// and the per-query kernel, bound by the random row gather, about 37 ns per
+// valid pair: the per-query path pays off only above a waste of about 5.
+constexpr int kSharedWaste = 4;
 
 static_assert(kListCap % kThreads == 0, "compaction split");
 static_assert(kRowsPerWave == 16, "one 16-row MFMA block per wave");
@@ -760,15 +762,22 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
 // tile order kernel
 // ============================================================================
 // One work-group sorts the tiles by descending step count (a counting sort:
-// keys are 0..kMaxTileKv/64, per-query tiles get key 0). The shared-row
-// kernel's work-group i runs tile order[i]; work-groups start in index order,
-// so the longest tiles start first and the short ones fill in at the end.
-// Tiles with equal keys may come in any order: each tile is independent.
+// a shared tile's key is 1 + its step count, a per-query tile's 0). The
+// shared-row kernel's work-group i runs entry i; work-groups start in index
+// order, so the longest tiles start first and the short ones fill in at the
+// end. Tiles with equal keys may come in any order: each tile is independent.
 // The queries of per-query tiles go to the per-query kernel's work list
 // (pq[0] = count, pq[1..] = flat query ids), in any order.
 constexpr int kOrderThreads = 1024;
-constexpr int kOrderKeys = int(sa::kMaxTileKv / kTileRows) + 1;
+constexpr int kOrderKeys = int(sa::kMaxTileKv / kTileRows) + 2;
 constexpr int kOrderKeysPadded = (kOrderKeys + 63) / 64 * 64;
+// An order entry is (key << kOrderTileBits) | tile: key 0 for a per-query
+// tile, else 1 + its step count, so the shared-row kernel learns its tile and
+// step count from one load. A plan has at most b * m / 4 <= 2^22 tiles.
+constexpr int kOrderTileBits = 22;
+static_assert(sa::kMaxUnits / (sa::kTileQueries / 2) <= (int64_t(1) << kOrderTileBits),
+              "tile ids fit the order entry");
+static_assert(kOrderKeys <= (1 << (31 - kOrderTileBits)), "keys fit the order entry");
 
 struct OrderParams {
   const int32_t* meta;
@@ -789,7 +798,7 @@ __global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const Orde
   __syncthreads();
   auto key = [&](int t) {
     const int32_t* mt = meta + int64_t(t) * kMetaInts;
-    return mt[1] == kModeShared ? (mt[0] + kTileRows - 1) / kTileRows : 0;
+    return mt[1] == kModeShared ? (mt[0] + kTileRows - 1) / kTileRows + 1 : 0;
   };
   for (int t = tid; t < ntiles; t += kOrderThreads) {
     const int k = key(t);
@@ -822,7 +831,10 @@ __global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const Orde
     }
   }
   __syncthreads();
-  for (int t = tid; t < ntiles; t += kOrderThreads) p.order[atomicAdd(&s_pos[key(t)], 1)] = t;
+  for (int t = tid; t < ntiles; t += kOrderThreads) {
+    const int k = key(t);
+    p.order[atomicAdd(&s_pos[k], 1)] = (k << kOrderTileBits) | t;
+  }
 }
 
 // ============================================================================
@@ -879,14 +891,13 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  const int64_t tile = p.order[blockIdx.x];
-  const int32_t* meta = p.meta + tile * kMetaInts;
-  if (meta[1] != kModeShared) return;
-  const int nU = meta[0];
+  const int32_t entry = p.order[blockIdx.x];  // one load: tile and step count
+  if ((entry >> kOrderTileBits) == 0) return;   // a per-query tile
+  const int64_t tile = entry & ((1 << kOrderTileBits) - 1);
+  const int nsteps = (entry >> kOrderTileBits) - 1;
   const int64_t bi = tile / p.tiles_per_b;
   const int64_t q0 = (tile % p.tiles_per_b) * kTQ;
   const int qt = int(min(int64_t(kTQ), p.m - q0));
-  const int nsteps = (nU + kTileRows - 1) / kTileRows;
   if (nsteps == 0) {
     // no valid slot in any query of the tile: the sink takes all the mass
     __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m;
@@ -1199,6 +1210,10 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 // ============================================================================
 // split-topk combine: one 64-thread work-group per (query, head)
 // ============================================================================
+// Parts are read in batches of kCombineBatch (every load of a batch issued
+// before any is used), so a query costs about one memory latency per batch.
+constexpr int kCombineBatch = 8;
+
 __global__ void __launch_bounds__(64) sa_combine_kernel(const CombineParams p) {
   const int64_t qid = blockIdx.x / kHeads;
   const int h = int(blockIdx.x % kHeads);
@@ -1213,23 +1228,34 @@ __global__ void __launch_bounds__(64) sa_combine_kernel(const CombineParams p) {
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-  for (int s = 0; s < p.nsplit; ++s) {
-    const float* ps = part + s * kPartFloats;
-    const float ms = ps[h];
-    if (ms == -INFINITY) continue;  // part without a valid slot
-    const float w = exp2f(ms - M);
-    L += w * ps[kHeads + h];
-    const float4* po = reinterpret_cast<const float4*>(ps + 2 * kHeads + h * kDim + d0);
-    const float4 v0 = po[0];
-    const float4 v1 = po[1];
-    acc[0] += w * v0.x;
-    acc[1] += w * v0.y;
-    acc[2] += w * v0.z;
-    acc[3] += w * v0.w;
-    acc[4] += w * v1.x;
-    acc[5] += w * v1.y;
-    acc[6] += w * v1.z;
-    acc[7] += w * v1.w;
+  for (int s0 = 0; s0 < p.nsplit; s0 += kCombineBatch) {
+    float ms[kCombineBatch], ls[kCombineBatch];
+    float4 v0[kCombineBatch], v1[kCombineBatch];
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      const int sp = min(s0 + u, p.nsplit - 1);  // past the end: re-read the last part, weight 0
+      const float* ps = part + sp * kPartFloats;
+      ms[u] = s0 + u < p.nsplit ? ps[h] : -INFINITY;
+      ls[u] = ps[kHeads + h];
+      const float4* po = reinterpret_cast<const float4*>(ps + 2 * kHeads + h * kDim + d0);
+      v0[u] = po[0];
+      v1[u] = po[1];
+    }
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      // a part without a valid slot (or past the end) has weight 0; its
+      // partials are never inf or NaN, so 0 * them is 0
+      const float w = ms[u] == -INFINITY ? 0.f : exp2f(ms[u] - M);
+      L += w * ls[u];
+      acc[0] += w * v0[u].x;
+      acc[1] += w * v0[u].y;
+      acc[2] += w * v0[u].z;
+      acc[3] += w * v0[u].w;
+      acc[4] += w * v1[u].x;
+      acc[5] += w * v1[u].y;
+      acc[6] += w * v1[u].z;
+      acc[7] += w * v1[u].w;
+    }
   }
   float lse;
   const float f = sink_fold(M, L, p.sink[h] * kLog2e, lse);

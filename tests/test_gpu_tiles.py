@@ -178,7 +178,11 @@ def test_per_query_work_list_matches_direct_launch(gpu_sa):
     q, kv, sink, idx, sc = rand_case(1, 300, 16384, 256, seed=21, minus1=0.1)
     o_l = run(q, kv, sink, idx, sc)
     o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY)
-    assert torch.equal(o_l, o_p)
+    # tiles 0..36 (8 random queries each: dense work ~8x the valid slots) run
+    # per query; the last tile's 4 queries are few enough to be shared
+    assert torch.equal(o_l[:, :296], o_p[:, :296])
+    d = (o_l.float() - o_p.float()).abs()
+    assert d.max().item() <= 2e-2
     sampled_check(o_l, q, kv, sink, idx, sc, [(0, t) for t in (0, 1, 150, 295, 296, 299)],
                   "work list")
 
@@ -188,8 +192,10 @@ def test_work_list_mixed_with_aborted_tile(gpu_sa):
     aborts at run time (scores jump far above its reference) in one call: the
     aborted tile's queries are appended to the work list by the tile kernel
     and computed by the per-query kernel launched next."""
-    # 256 queries (as many as CUs, so the plan does not split them)
-    q, kv, sink, idx, sc = rand_case(1, 256, 2048, 512, seed=22)
+    # 256 queries (as many as CUs, so the plan does not split them); 512
+    # random rows of 8192 per query leave a tile's dense work ~7.6x its valid
+    # slots, so those tiles go to the per-query kernel
+    q, kv, sink, idx, sc = rand_case(1, 256, 8192, 512, seed=22)
     # queries 0..31: overlapping windows (shared tiles); 32..255 stay random
     # (per-query tiles from the index kernel)
     for t in range(32):
