@@ -315,20 +315,43 @@ __device__ __forceinline__ float wave_sum16(float x) {
 // ============================================================================
 // per-query kernel
 // ============================================================================
+// The rows of a part stream through a ring of kQRing LDS buffers of kQRows
+// rows each, filled by LDS-DMA (one 1 KiB row per wave instruction). While
+// the work-group computes on one buffer, the gathers of the next kQAhead
+// steps are in flight (96 KiB per work-group), so a short part (decode) has
+// its whole gather issued within its first steps, and a long one keeps
+// enough bytes in flight per CU to run at the random-row gather rate.
+constexpr int kQRows = 32;
+constexpr int kQRing = 4;
+constexpr int kQAhead = kQRing - 1;
+constexpr int kQRowsPerWave = kQRows / kWaves;  // rows of a step each wave gathers
+static_assert(kQAhead == 3 && kQRowsPerWave == 8, "the vmcnt waits of the ring");
+
 struct QuerySmem {
-  uint8_t tile[2][kTileRows * kRowStride];
+  uint8_t tile[kQRing][kQRows * kRowStride];
   int32_t list[kListCap];
-  __bf16 p[kHeads * kTileRows];
+  __bf16 p[kHeads * kQRows];
   float red[kWaves][kHeads];
   int cnt[kWaves];
 };
+
+// Waits until at most the gathers of `later` (0..2) steps issued after the
+// current one are outstanding: this wave's rows of the current step are in
+// LDS. Loads return in order, and each step is kQRowsPerWave loads per wave.
+__device__ __forceinline__ void wait_ring(int later) {
+  if (later >= 2)
+    asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+  else if (later == 1)
+    asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 
 // One (query, topk part) unit of the per-query kernel. Leaves every wave past
 // its last LDS access of `sm` only after the work-group's final barrier, so a
 // following unit may reuse `sm` after one more __syncthreads().
 __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t unit,
                                            QuerySmem& sm) {
-  auto& s_tile = sm.tile;
   auto& s_list = sm.list;
   auto& s_p = sm.p;
   auto& s_red = sm.red;
@@ -336,7 +359,7 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15;   // MFMA column lane: head (S^T, P) or d (O)
   const int g = lane >> 4;   // MFMA k-group
 
@@ -348,7 +371,8 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
   const int64_t s_end = min(p.topk, s_begin + p.split_len);
 
   // Q^T as the B operand of S^T = K . Q^T: lane (n, g) holds head n,
-  // d = 32s + 8g .. 32s + 8g + 7 for k-step s.
+  // d = 32s + 8g .. 32s + 8g + 7 for k-step s. Issued first, so the
+  // compaction's wait for the indices covers it.
   bf16x8 qf[kDim / 32];
   {
     const __bf16* qrow = p.q + bi * p.sq_b + mi * p.sq_m + int64_t(n) * p.sq_h + 8 * g;
@@ -357,8 +381,12 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
       qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
   }
 
-  const __bf16* kvb = p.kv + bi * p.skv_b;
+  const uint8_t* kvb = reinterpret_cast<const uint8_t*>(p.kv + bi * p.skv_b);
+  const int64_t row_bytes = p.skv_n * 2;
   const int32_t* irow = p.idx + bi * p.si_b + mi * p.si_m;
+  // LDS address of this wave's first row in ring buffer 0
+  const uint32_t lds_rows = __builtin_amdgcn_readfirstlane(uint32_t(
+      reinterpret_cast<uintptr_t>((lds_u8_t*)&sm.tile[0][wave * kQRowsPerWave * kRowStride])));
 
   float m_run = -INFINITY;  // running max (log2 domain) of head n
   float l_run = 0.f;        // this lane's share of the running sum of head n
@@ -368,7 +396,7 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
 
   for (int64_t base = s_begin; base < s_end; base += kListCap) {
     const int cnt = int(min(int64_t(kListCap), s_end - base));
-    __syncthreads();  // the previous batch is done with s_list
+    __syncthreads();  // the previous batch is done with s_list and the ring
     // ---- compaction of this batch's valid slots -----------------------------
     int vals[kSlotsPerThread];
     int c = 0;
@@ -405,59 +433,57 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
       if (vals[i] >= 0) s_list[pos++] = vals[i];
     __syncthreads();
     if (nvalid == 0) continue;
-    const int nsteps = (nvalid + kTileRows - 1) / kTileRows;
+    const int nsteps = (nvalid + kQRows - 1) / kQRows;
 
-    // ---- gather pipeline -----------------------------------------------------
-    // wave w fetches tile rows 16w..16w+15; lane l moves bytes 16l..16l+15.
-    bf16x8 pref[kRowsPerWave];
-    auto fetch = [&](int step) {
+    // ---- gather ring -----------------------------------------------------------
+    // Wave w gathers rows 8w..8w+7 of a step; lane i < 8 reads the list entry
+    // of row i, and each row's address is a scalar base (readlane). Entries
+    // past the last valid one take entry 0's row; their scores are masked.
+    auto issue = [&](int step) {
+      const int e = step * kQRows + wave * kQRowsPerWave + (lane & 7);
+      const int rv = s_list[e < nvalid ? e : 0];
+      const uint32_t lbase = lds_rows + uint32_t((step % kQRing) * kQRows * kRowStride);
 #pragma unroll
-      for (int i = 0; i < kRowsPerWave; ++i) {
-        const int e = step * kTileRows + wave * kRowsPerWave + i;
-        const int row = s_list[e < nvalid ? e : 0];  // tail rows: any valid row, masked
-        pref[i] = *reinterpret_cast<const bf16x8*>(kvb + int64_t(row) * p.skv_n + 8 * lane);
+      for (int i = 0; i < kQRowsPerWave; ++i) {
+        const int row = __builtin_amdgcn_readlane(rv, i);
+        lds_dma_row(kvb + int64_t(row) * row_bytes, 16 * lane, lbase + uint32_t(i * kRowStride));
       }
     };
-    auto stash = [&](int buf) {
-#pragma unroll
-      for (int i = 0; i < kRowsPerWave; ++i)
-        *reinterpret_cast<bf16x8*>(&s_tile[buf][(wave * kRowsPerWave + i) * kRowStride + 16 * lane]) =
-            pref[i];
-    };
-    fetch(0);
-    stash(0);
-    __syncthreads();
+    for (int s = 0; s < min(kQAhead, nsteps); ++s) issue(s);
 
     for (int step = 0; step < nsteps; ++step) {
-      const uint8_t* tb = s_tile[step & 1];
-      const bool more = step + 1 < nsteps;
-      if (more) fetch(step + 1);
+      wait_ring(min(nsteps - 1, step + kQAhead - 1) - step);
+      lds_barrier();  // every wave's rows of `step` are in LDS; the previous buffer is free
+      if (step + kQAhead < nsteps) issue(step + kQAhead);
+      const uint8_t* tb = sm.tile[step % kQRing];
 
-      // ---- S^T = K . Q^T for rows 16w + (0..15) ------------------------------
+      // ---- S^T = K . Q^T for this wave's 8 rows ----------------------------------
+      // MFMA rows 8..15 repeat rows 0..7 (the A operand reads row n & 7).
       f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
       {
-        const uint8_t* krow = tb + (wave * kRowsPerWave + n) * kRowStride + 16 * g;
+        const uint8_t* krow = tb + (wave * kQRowsPerWave + (n & 7)) * kRowStride + 16 * g;
 #pragma unroll
         for (int s = 0; s < kDim / 32; ++s) {
           const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 64 * s);
           sacc = mfma_16x16x32(kf, qf[s], sacc);
         }
       }
-      // lane (n, g) now holds S[head n][tile row 16w + 4g + j], j = 0..3
+      // lane (n, g) now holds S[head n][row 8w + 4g + j], j = 0..3; lanes with
+      // g >= 2 hold the repeated rows and drop them
 
       // ---- online softmax ------------------------------------------------------
-      const int rbase = step * kTileRows + wave * kRowsPerWave + 4 * g;
+      const int rbase = step * kQRows + wave * kQRowsPerWave + 4 * g;
       float sv[4];
       float mx = -INFINITY;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        sv[j] = (rbase + j < nvalid) ? sacc[j] * p.scale_log2 : -INFINITY;
+        sv[j] = (g < 2 && rbase + j < nvalid) ? sacc[j] * p.scale_log2 : -INFINITY;
         mx = fmaxf(mx, sv[j]);
       }
       mx = wave_max16(mx);
       if (g == 0) s_red[wave][n] = mx;
       lds_barrier();
-      // finite: every tile holds at least one valid row
+      // finite: the step's first row is valid (wave 0)
       const float mstep = fmaxf(fmaxf(s_red[0][n], s_red[1][n]), fmaxf(s_red[2][n], s_red[3][n]));
       float alpha = 1.f;
       if (mstep > m_run + kRescaleLog2) {
@@ -473,7 +499,7 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
         pb[j] = static_cast<__bf16>(pj);
       }
       l_run = l_run * alpha + psum;
-      *reinterpret_cast<bf16x4*>(&s_p[n * kTileRows + wave * kRowsPerWave + 4 * g]) = pb;
+      if (g < 2) *reinterpret_cast<bf16x4*>(&s_p[n * kQRows + wave * kQRowsPerWave + 4 * g]) = pb;
       if (__any(alpha != 1.f)) {
         float aj[4];
 #pragma unroll
@@ -483,15 +509,13 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
 #pragma unroll
           for (int j = 0; j < 4; ++j) oacc[blk][j] *= aj[j];
       }
-      lds_barrier();
+      lds_barrier();  // P of every wave is in LDS
 
-      // ---- O[:, 128w .. 128w+127] += P . V -------------------------------------
-#pragma unroll
-      for (int kk = 0; kk < kTileRows / 32; ++kk) {
-        const bf16x8 pf =
-            *reinterpret_cast<const bf16x8*>(&s_p[n * kTileRows + 32 * kk + 8 * g]);
-        const uint8_t* vb = tb + (32 * kk + 8 * g + (n >> 2)) * kRowStride +
-                            (wave * kDPerWave + 4 * (n & 3)) * 2;
+      // ---- O[:, 128w .. 128w+127] += P . V over the step's 32 rows ---------------
+      {
+        const bf16x8 pf = *reinterpret_cast<const bf16x8*>(&s_p[n * kQRows + 8 * g]);
+        const uint8_t* vb =
+            tb + (8 * g + (n >> 2)) * kRowStride + (wave * kDPerWave + 4 * (n & 3)) * 2;
 #pragma unroll
         for (int blk = 0; blk < kDBlocks; ++blk) {
           const bf16x4 v0 = lds_read_tr16(vb + blk * 32);
@@ -500,8 +524,6 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
           oacc[blk] = mfma_16x16x32(pf, vf, oacc[blk]);
         }
       }
-      if (more) stash((step + 1) & 1);
-      lds_barrier();
     }
   }
 
@@ -1210,8 +1232,10 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 // ============================================================================
 // split-topk combine: one 64-thread work-group per (query, head)
 // ============================================================================
-// Parts are read in batches of kCombineBatch (every load of a batch issued
-// before any is used), so a query costs about one memory latency per batch.
+// Parts are read in batches of kCombineBatch, every load of a batch issued
+// before any is used, and merged with a running max (the accumulators are
+// rescaled when a batch raises it), so a query costs one memory latency per
+// batch.
 constexpr int kCombineBatch = 8;
 
 __global__ void __launch_bounds__(64) sa_combine_kernel(const CombineParams p) {
@@ -1223,7 +1247,6 @@ __global__ void __launch_bounds__(64) sa_combine_kernel(const CombineParams p) {
   const float* part = p.part + qid * p.nsplit * kPartFloats;
 
   float M = -INFINITY;
-  for (int s = 0; s < p.nsplit; ++s) M = fmaxf(M, part[s * kPartFloats + h]);
   float L = 0.f;
   float acc[8];
 #pragma unroll
@@ -1235,11 +1258,24 @@ __global__ void __launch_bounds__(64) sa_combine_kernel(const CombineParams p) {
     for (int u = 0; u < kCombineBatch; ++u) {
       const int sp = min(s0 + u, p.nsplit - 1);  // past the end: re-read the last part, weight 0
       const float* ps = part + sp * kPartFloats;
-      ms[u] = s0 + u < p.nsplit ? ps[h] : -INFINITY;
+      ms[u] = ps[h];
       ls[u] = ps[kHeads + h];
       const float4* po = reinterpret_cast<const float4*>(ps + 2 * kHeads + h * kDim + d0);
       v0[u] = po[0];
       v1[u] = po[1];
+    }
+    float Mb = M;
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      if (s0 + u >= p.nsplit) ms[u] = -INFINITY;
+      Mb = fmaxf(Mb, ms[u]);
+    }
+    if (Mb != M) {  // the batch raised the max: rescale (M = -inf: nothing merged yet)
+      const float r = M == -INFINITY ? 0.f : exp2f(M - Mb);
+      L *= r;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] *= r;
+      M = Mb;
     }
 #pragma unroll
     for (int u = 0; u < kCombineBatch; ++u) {
