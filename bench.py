@@ -101,8 +101,7 @@ def time_calls(fn, sets, scale, steps, warmup):
 
 def kernel_times(sets, scale, steps, warmup):
     """Average launch duration (ms) of each kernel over `steps` calls, from
-    the HIP events sa_forward_events records on the calls' stream, and the
-    per-tile modes of the last call (None without a shared-row plan)."""
+    the HIP events sa_forward_events records on the calls' stream."""
     import sa_capi
     lib = sa_capi.load()
     stream = torch.cuda.current_stream()
@@ -130,28 +129,7 @@ def kernel_times(sets, scale, steps, warmup):
              if (masks[i] >> k) & 1]
         if d:
             times[name] = sum(d) / len(d)
-    modes = None
-    if "tile" in times:      # the index kernel's per-tile meta sits at workspace offset 0
-        q = sets[0][0]
-        ntiles = q.shape[0] * ((q.shape[1] + 7) // 8)
-        modes = ws[: ntiles * 16].view(torch.int32).view(ntiles, 4)[:, 1].cpu()
-    return times, modes
-
-
-def kernel_share(idx_cpu, modes, kernel):
-    """Valid slots processed by `kernel` ("tile" or "query") in the last call."""
-    valid = (idx_cpu != -1).sum(dim=2)                  # [b, m]
-    n_all = int(valid.sum())
-    if modes is None:
-        return n_all if kernel != "tile" else 0
-    b, m = valid.shape
-    tpb = (m + 7) // 8
-    shared = torch.zeros(b, m, dtype=torch.bool)
-    for t in torch.nonzero(modes == 1).flatten().tolist():
-        bi, j = divmod(t, tpb)
-        shared[bi, 8 * j: 8 * j + 8] = True
-    n_tile = int(valid[shared].sum())
-    return n_tile if kernel == "tile" else n_all - n_tile
+    return times
 
 
 def cpu_baseline(cpu_inputs, target_s=4.0, runs=3):
@@ -193,15 +171,14 @@ def cpu_baseline(cpu_inputs, target_s=4.0, runs=3):
             "us_per_call_extrapolated": round(dt / nq * b * m * 1e6, 1)}
 
 
-def roofline(name, idx_cpu, b, m, flops, compulsory, n_valid, times, modes):
+def roofline(name, flops, compulsory, times):
+    """The dominant kernel's algorithmic rate. A call launches either the
+    shared-row kernel (which also runs the queries of per-query tiles) or the
+    per-query kernel, so the dominant one processes every valid slot."""
     dom = max(times, key=times.get)
     t = times[dom] * 1e-3
     mfma_bound = flops / (PEAK_MFMA_TFLOPS * 1e12) >= compulsory / (PEAK_HBM_GBPS * 1e9)
-    share = 0.0
-    if dom in ("tile", "query"):
-        share = kernel_share(idx_cpu, modes, dom) / max(n_valid, 1)
-    elif dom == "combine":
-        share = 1.0
+    share = 1.0 if dom in ("tile", "query", "combine") else 0.0
     if mfma_bound:
         ach = flops * share / t / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_MFMA_TFLOPS,
@@ -229,7 +206,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
     cfg = wl.CONFIGS[name]
     n_valid, flops, gathered, uniq, compulsory = algorithmic(idx, b, m)
     ms = time_calls(submission.sparse_attn, sets, scale, steps, warmup)
-    times, modes = kernel_times(sets, scale, steps, warmup)
+    times = kernel_times(sets, scale, steps, warmup)
     t = ms * 1e-3
     tflops = flops / t / 1e12
     gbps = gathered / t / 1e9
@@ -255,7 +232,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
                    "n_valid": n_valid, "unique_rows": uniq,
                    "flops_alg": flops, "gathered_bytes": gathered,
                    "compulsory_bytes": compulsory, "input_sets_rotated": nsets},
-        "roofline": roofline(name, idx, b, m, flops, compulsory, n_valid, times, modes),
+        "roofline": roofline(name, flops, compulsory, times),
     }
     rec["cpu_baseline"] = cpu_baseline(cpu_inputs) if with_cpu else None
     del sets

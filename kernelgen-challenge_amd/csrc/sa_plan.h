@@ -176,8 +176,8 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
     p.cnts_off = off;  // fp16 log2 multiplicity per (union entry, tile query)
     off = round_up(off + size_t(p.ntiles) * p.tile_cap * kTileQueries * 2, 256);
-    p.pq_off = off;    // per-query work list: count, then up to b * m query ids
-    off = round_up(off + size_t(1 + p.units) * 4, 256);
+    p.pq_off = off;    // per-query work list: count, shared tiles, then up to b * m query ids
+    off = round_up(off + size_t(2 + p.units) * 4, 256);
   }
   if (p.nsplit > 1) {
     p.part_off = off;

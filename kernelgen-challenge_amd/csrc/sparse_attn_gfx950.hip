@@ -106,10 +106,6 @@ struct FwdParams {
   __bf16* o;
   float* part;          // [units * nsplit] x (ml[32] + O[16*512]) when split
   int32_t* err;
-  // Non-null with a shared-row plan: pq[0] is the number of queries left to
-  // this kernel and pq[1..] their flat ids b * m + m_i; the grid strides over
-  // them. Null: work-group i runs unit i (query i / nsplit, part i % nsplit).
-  const int32_t* pq;
   int64_t m, kv_len, topk;
   int64_t sq_b, sq_m, sq_h;
   int64_t skv_b, skv_n;
@@ -142,10 +138,10 @@ struct TileParams {
   const __bf16* kv;
   const float* sink;
   __bf16* o;
-  const int32_t* meta;
-  int32_t* meta_out;    // same array: a tile that must rescale marks itself per-query
-  int32_t* pq;          // ... and appends its queries to the per-query work list
-  const int32_t* order; // work-group i runs tile order[i]
+  // Per-query work list of the order kernel: pq[0] = number of queries,
+  // pq[1] = number of shared tiles, pq[2..] = flat query ids b * m + m_i.
+  const int32_t* pq;
+  const int32_t* order; // work-group i < ntiles runs entry order[i]
   const uint32_t* row_off;
   const _Float16* lcnt;
   int64_t m, cap, tiles_per_b;
@@ -155,7 +151,8 @@ struct TileParams {
   float scale_log2;
   float* lse;           // fp32 [b, m, h] or null
   int64_t sl_b, sl_m, sl_h;
-  int64_t nblocks;
+  int64_t ntiles;
+  FwdParams fwd;        // the per-query kernel's arguments (nsplit = 1)
 };
 
 struct CombineParams {
@@ -566,20 +563,10 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
   }
 }
 
-// kListed = false: work-group i runs unit i. kListed = true (shared-row
-// plans): the grid strides over the work list p.pq.
-template <bool kListed>
+// Work-group i runs unit i (query i / nsplit, part i % nsplit).
 __global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdParams p) {
   __shared__ __attribute__((aligned(16))) QuerySmem sm;
-  if constexpr (!kListed) {
-    query_unit(p, blockIdx.x, sm);
-  } else {
-    const int nu = __builtin_amdgcn_readfirstlane(p.pq[0]);
-    for (int k = blockIdx.x; k < nu; k += gridDim.x) {
-      query_unit(p, p.pq[1 + k], sm);
-      __syncthreads();  // every wave is done with sm before the next unit
-    }
-  }
+  query_unit(p, blockIdx.x, sm);
 }
 
 // ============================================================================
@@ -830,11 +817,14 @@ __global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const Orde
       const int64_t q0 = (t % p.tiles_per_b) * kTQ;
       const int qt = int(min(int64_t(kTQ), p.m - q0));
       const int pos = atomicAdd(&s_npq, qt);
-      for (int j = 0; j < qt; ++j) p.pq[1 + pos + j] = int32_t(bi * p.m + q0 + j);
+      for (int j = 0; j < qt; ++j) p.pq[2 + pos + j] = int32_t(bi * p.m + q0 + j);
     }
   }
   __syncthreads();
-  if (tid == 0) p.pq[0] = s_npq;
+  if (tid == 0) {
+    p.pq[0] = s_npq;
+    p.pq[1] = ntiles - s_pos[0];  // shared tiles: every key above 0
+  }
   if (tid < 64) {
     // exclusive scan over descending keys: the start of key k is the number
     // of tiles with a larger key
@@ -901,11 +891,25 @@ constexpr int kKRing = SA_K_RING;
 constexpr int kDmaEvery = SA_DMA_EVERY;
 static_assert(kDmaEvery * 16 <= 2 * (kDim / 16), "the gathers fit in the S^T MFMAs");
 
+struct TileSmem {
+  uint8_t tile[2][kTileRows * kTilePitch];
+  uint8_t p[kTileCols * kPPitch];
+  _Float16 lc[2][kTQ * kTileRows];
+  int abort;
+};
+// The tile kernel's work-groups either run a shared tile or, as per-query
+// workers, query units: the two layouts share the LDS.
+union TileQuerySmem {
+  TileSmem t;
+  QuerySmem q;
+};
+
 __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t s_tile[2][kTileRows * kTilePitch];
-  __shared__ __attribute__((aligned(16))) uint8_t s_p[kTileCols * kPPitch];
-  __shared__ __attribute__((aligned(16))) _Float16 s_lc[2][kTQ * kTileRows];
-  __shared__ int s_abort;
+  __shared__ __attribute__((aligned(16))) TileQuerySmem sm;
+  auto& s_tile = sm.t.tile;
+  auto& s_p = sm.t.p;
+  auto& s_lc = sm.t.lc;
+  auto& s_abort = sm.t.abort;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -913,8 +917,20 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  const int32_t entry = p.order[blockIdx.x];  // one load: tile and step count
-  if ((entry >> kOrderTileBits) == 0) return;   // a per-query tile
+  // one load: tile and step count (work-groups past the order are workers)
+  const int32_t entry = blockIdx.x < p.ntiles ? p.order[blockIdx.x] : 0;
+  if ((entry >> kOrderTileBits) == 0) {
+    // Per-query worker: the work-groups from the first per-query tile's
+    // order entry to the end of the grid stride over the work list.
+    const int nq = __builtin_amdgcn_readfirstlane(p.pq[0]);
+    const int nshared = __builtin_amdgcn_readfirstlane(p.pq[1]);
+    const int workers = int(gridDim.x) - nshared;
+    for (int k = int(blockIdx.x) - nshared; k < nq; k += workers) {
+      query_unit(p.fwd, p.pq[2 + k], sm.q);
+      __syncthreads();  // every wave is done with the LDS before the next unit
+    }
+    return;
+  }
   const int64_t tile = entry & ((1 << kOrderTileBits) - 1);
   const int nsteps = (entry >> kOrderTileBits) - 1;
   const int64_t bi = tile / p.tiles_per_b;
@@ -1182,12 +1198,13 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 
     dma_barrier();  // every wave's prefetch has landed; P and this tile are free
     if (abort_seen != 0) {  // uniform: every wave read it after the same barrier
-      if (tid == 0) {       // the per-query kernel, launched next, takes the tile's queries
-        p.meta_out[tile * kMetaInts + 1] = sa::kModePerQuery;
-        const int pos = atomicAdd(p.pq, qt);
-        for (int j = 0; j < qt; ++j) p.pq[1 + pos + j] = int32_t(bi * p.m + q0 + j);
+      // The tile's queries run per query here (online rescale); nothing of
+      // the tile was written and no transfer is in flight.
+      for (int j = 0; j < qt; ++j) {
+        query_unit(p.fwd, bi * p.m + q0 + j, sm.q);
+        __syncthreads();
       }
-      return;               // no o written; no transfer in flight
+      return;
     }
   }
 
@@ -1552,8 +1569,6 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.kv = p.kv;
     tp.sink = a->sink;
     tp.o = p.o;
-    tp.meta = ip.meta;
-    tp.meta_out = ip.meta;
     tp.pq = pq;
     tp.order = order;
     tp.row_off = ip.row_off;
@@ -1574,25 +1589,21 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.sl_b = a->slse[0];
     tp.sl_m = a->slse[1];
     tp.sl_h = a->slse[2];
-    tp.nblocks = plan.ntiles;
+    tp.ntiles = plan.ntiles;
+    tp.fwd = p;
+    // One work-group per tile, then one per compute unit more: the queries of
+    // per-query tiles are run by the work-groups of those tiles' order
+    // entries and these (an empty work list costs them one read each).
     if (!mark(SA_KERNEL_TILE, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), 0,
+    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles + cus)), dim3(kThreads), 0,
                        stream, tp);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
     if (!mark(SA_KERNEL_TILE, 1)) return SA_EHIP;
-    // the per-query kernel strides over the work list with one work-group
-    // per compute unit (its LDS allows one per CU)
-    p.pq = pq;
-    p.nblocks = min(p.nblocks, int64_t(cus));
+    return SA_OK;
   }
 
   if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
-  if (p.pq != nullptr)
-    hipLaunchKernelGGL(sa_fwd_query_kernel<true>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
-                       stream, p);
-  else
-    hipLaunchKernelGGL(sa_fwd_query_kernel<false>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
-                       stream, p);
+  hipLaunchKernelGGL(sa_fwd_query_kernel, dim3(unsigned(p.nblocks)), dim3(kThreads), 0, stream, p);
   if (hipGetLastError() != hipSuccess) return SA_EHIP;
   if (!mark(SA_KERNEL_QUERY, 1)) return SA_EHIP;
   if (plan.nsplit > 1) {

@@ -246,12 +246,13 @@ def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
         assert p["tile_cap"] % 64 == 0 and p["tile_cap"] >= min(kv_len, 8 * topk)
         # per tile: meta, its slot in the launch order, a 32-bit offset per
         # union row and an fp16 log2 multiplicity per (query, union row); then
-        # the per-query work list (a count and up to b * m query ids)
-        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 2 * 8) * p["tile_cap"]) + 4 * (1 + b * m)
+        # the per-query work list (a count, the shared-tile count and up to
+        # b * m query ids)
+        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 2 * 8) * p["tile_cap"]) + 4 * (2 + b * m)
         regions = [(p["meta_off"], 16 * p["ntiles"]), (p["order_off"], 4 * p["ntiles"]),
                    (p["rows_off"], 4 * p["ntiles"] * p["tile_cap"]),
                    (p["cnts_off"], 2 * 8 * p["ntiles"] * p["tile_cap"]),
-                   (p["pq_off"], 4 * (1 + b * m))]
+                   (p["pq_off"], 4 * (2 + b * m))]
         for (o0, n0), (o1, _) in zip(regions, regions[1:]):
             assert o0 % 256 == 0 and o0 + n0 <= o1           # aligned, disjoint, in order
         assert regions[-1][0] + regions[-1][1] <= p["ws"]
