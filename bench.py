@@ -57,7 +57,7 @@ KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel"
 # FETCH_SIZE x 2.0000, WRITE_SIZE x 1.0000). Commands and raw figures:
 # profiles/sa_fwd_tile_kernel_causal_prefill_pmc_traffic.txt. Measured for
 # the kernels as built; a workload without an entry reports null.
-TRAFFIC = {"causal_prefill": 206303858}
+TRAFFIC = {"causal_prefill": 206151533}
 
 
 def algorithmic(idx_cpu: torch.Tensor, b, m):

@@ -33,8 +33,8 @@ constexpr int kMetaInts = 4;  // per tile: union size, mode, valid slots, spare
 //  * shared-row path (`tiles`): an index kernel builds each tile's row union,
 //    a one-work-group pass orders the tiles by descending step count (longest
 //    first, so the last work-groups to start are the short ones), then tiles
-//    whose queries overlap enough run in the shared-row kernel and the rest in
-//    the per-query kernel.
+//    whose queries overlap enough run in the shared-row kernel and the rest
+//    per query, by that kernel's remaining work-groups.
 struct Plan {
   int64_t units;       // b * m
   int nsplit;          // parts per query (1 = no combine pass)

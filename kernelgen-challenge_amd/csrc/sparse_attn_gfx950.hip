@@ -28,20 +28,21 @@
 //   with each wave owning a quarter of d; v_mfma_f32_32x32x16_bf16; the
 //   softmax of one 32-row half runs between the MFMAs of the next. A fixed
 //   per-column reference replaces rescaling; a tile whose scores jump above
-//   it hands itself to the per-query kernel.
+//   it runs its queries per query in place. The work-groups past the shared
+//   tiles (and one per CU more) run the queries of per-query tiles.
 // sa_fwd_query_kernel  one work-group (4 wave64s) per (query, topk part):
-//   compacts the part's valid indices into LDS, then loops over tiles of 64
-//   gathered rows double-buffered in LDS (each row one coalesced 1 KiB wave
-//   load, prefetched a step ahead into registers). S^T = K . Q^T with
-//   v_mfma_f32_16x16x32_bf16 (wave w: tile rows 16w.., 16 heads, K = d = 512,
-//   Q^T resident in registers); online softmax with a per-head max across
-//   the waves through LDS; O += P . V with the same MFMA (wave w: d columns
-//   128w..), its V operands read from the same LDS rows by
-//   ds_read_b64_tr_b16 transposing reads. Writes bf16 o, or per-part
-//   (max, sum, unnormalised O) for sa_combine_kernel. Skips queries of
-//   shared tiles.
+//   compacts the part's valid indices into LDS, then streams steps of 32
+//   gathered rows through a ring of 4 LDS buffers filled by LDS-DMA (three
+//   steps in flight). S^T = K . Q^T with v_mfma_f32_16x16x32_bf16 (wave w:
+//   the step's rows 8w.., 16 heads, K = d = 512, Q^T resident in registers);
+//   online softmax with a per-head max across the waves through LDS;
+//   O += P . V with the same MFMA (wave w: d columns 128w..), its V operands
+//   read from the same LDS rows by ds_read_b64_tr_b16 transposing reads.
+//   Writes bf16 o, or per-part (max, sum, unnormalised O) for
+//   sa_combine_kernel.
 // sa_combine_kernel  merges the topk parts of one (query, head), folds the
 //   sink and stores bf16.
+// sa_merge_kernel  merges caller-supplied (o, lse) partials (sa_merge).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -74,7 +75,8 @@ constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kRescaleLog2 = 8.f;
 // Shared tiles never rescale O: scores may exceed a column's fixed reference
 // by up to this (log2 units; weights <= 255 * 2^24 stay far from fp32 and
-// bf16 overflow). A larger jump sends the tile to the per-query kernel.
+// bf16 overflow). A larger jump makes the tile run its queries per query
+// (online rescale) instead.
 constexpr float kTileMaxJump = 24.f;
 
 constexpr int kTQ = sa::kTileQueries;       // queries per shared tile
@@ -152,7 +154,7 @@ struct TileParams {
   float* lse;           // fp32 [b, m, h] or null
   int64_t sl_b, sl_m, sl_h;
   int64_t ntiles;
-  FwdParams fwd;        // the per-query kernel's arguments (nsplit = 1)
+  FwdParams fwd;        // arguments of the queries run per query (nsplit = 1)
 };
 
 struct CombineParams {
@@ -775,8 +777,9 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
 // shared-row kernel's work-group i runs entry i; work-groups start in index
 // order, so the longest tiles start first and the short ones fill in at the
 // end. Tiles with equal keys may come in any order: each tile is independent.
-// The queries of per-query tiles go to the per-query kernel's work list
-// (pq[0] = count, pq[1..] = flat query ids), in any order.
+// The queries of per-query tiles go to the work list of the shared-row
+// kernel's per-query workers (pq[0] = count, pq[1] = number of shared tiles,
+// pq[2..] = flat query ids), in any order.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderKeys = int(sa::kMaxTileKv / kTileRows) + 2;
 constexpr int kOrderKeysPadded = (kOrderKeys + 63) / 64 * 64;
@@ -1062,7 +1065,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     } else if (k == 10) {
       // Fixed reference: a column keeps the max of its first non-empty half.
       // A later score more than kTileMaxJump above it would need O rescaled;
-      // the tile then hands itself to the per-query kernel.
+      // the tile then runs its queries per query instead.
       abort_any |= __any(m_run != -INFINITY && mx > m_run + kTileMaxJump) != 0;
       if (m_run == -INFINITY) m_run = mx;
       mref = m_run == -INFINITY ? 0.f : m_run;  // column still empty
