@@ -9,14 +9,17 @@ headline metric is quoted on. Calls rotate over ``--sets`` distinct input
 sets (separate q/kv/o buffers) so no call finds the previous call's data in
 the caches.
 
-Two timed loops of K calls each, both bracketed by ``torch.cuda.synchronize()``:
+Three timed loops of K calls each, all bracketed by ``torch.cuda.synchronize()``:
   1. whole calls through the drop-in (``submission.sparse_attn``), timed with
      HIP events on the stream the kernels run on -> ``value``, ``ms_per_step``;
   2. the same calls through the C-ABI's event hook (``sa_forward_events``),
      which records HIP events on that stream around every kernel it launches
      -> the average launch duration of each kernel; the longest is the
      dominant kernel, whose algorithmic work per launch / duration is
-     ``roofline.achieved``.
+     ``roofline.achieved``;
+  3. the calls of loop 1 with each input set's index plan
+     (``sparse_attn_plan``) made before the loop -> ``planned``: the cost of
+     a call whose indices are reused (not the headline ``value``).
 
 Printed: ONE JSON line (stdout). ``--all`` also prints one line per other
 configuration on stderr. ``--copy-calibration`` runs a plain device copy of
@@ -83,17 +86,23 @@ def make_sets(name, nsets, dev):
     return cpu, sets
 
 
-def time_calls(fn, sets, scale, steps, warmup):
-    for i in range(warmup):
+def time_calls(fn, sets, scale, steps, warmup, plans=None):
+    """ms per call of fn over the rotated input sets (with plans[i] for set i
+    passed as plan=, when given)."""
+    def call(i):
         s = sets[i % len(sets)]
-        fn(s[0], s[1], s[2], s[3], scale)
+        if plans is None:
+            fn(s[0], s[1], s[2], s[3], scale)
+        else:
+            fn(s[0], s[1], s[2], s[3], scale, plan=plans[i % len(sets)])
+    for i in range(warmup):
+        call(i)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
     for i in range(steps):
-        s = sets[i % len(sets)]
-        fn(s[0], s[1], s[2], s[3], scale)
+        call(i)
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps  # ms per call
@@ -207,6 +216,11 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
     n_valid, flops, gathered, uniq, compulsory = algorithmic(idx, b, m)
     ms = time_calls(submission.sparse_attn, sets, scale, steps, warmup)
     times = kernel_times(sets, scale, steps, warmup)
+    # the same calls with each input set's index plan made beforehand
+    # (sparse_attn_plan): what a call costs when its indices are reused
+    plans = [submission.sparse_attn_plan(s[0], s[1], s[3]) for s in sets]
+    ms_planned = time_calls(submission.sparse_attn, sets, scale, steps, warmup, plans=plans)
+    del plans
     t = ms * 1e-3
     tflops = flops / t / 1e12
     gbps = gathered / t / 1e9
@@ -233,6 +247,9 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
                    "flops_alg": flops, "gathered_bytes": gathered,
                    "compulsory_bytes": compulsory, "input_sets_rotated": nsets},
         "roofline": roofline(name, flops, compulsory, times),
+        "planned": {"us_per_call": round(ms_planned * 1e3, 2),
+                    "value": round(flops / (ms_planned * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+                    "note": "index plan made before the timed calls and reused"},
     }
     rec["cpu_baseline"] = cpu_baseline(cpu_inputs) if with_cpu else None
     del sets

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 2
+#define SA_ABI_VERSION 3
 
 /* Return codes. */
 enum {
@@ -54,7 +54,10 @@ enum {
   SA_FLAG_PER_QUERY = 1u,
   /* run every eligible tile of consecutive queries through the shared-row
      kernel, whatever the overlap of their indices */
-  SA_FLAG_FORCE_TILES = 2u
+  SA_FLAG_FORCE_TILES = 2u,
+  /* (ABI version 3) the workspace holds the index plan of these arguments,
+     made by sa_plan_indices: the index-dependent kernels are skipped */
+  SA_FLAG_PLANNED = 4u
 };
 
 /*
@@ -151,6 +154,25 @@ typedef struct sa_merge_args {
  * return before any device work.
  */
 int sa_merge(const sa_merge_args* a, void* hip_stream);
+
+/*
+ * Index preprocessing on its own (ABI version 3). Runs the index-dependent
+ * part of sa_forward into a->workspace (sa_workspace_bytes of the same
+ * arguments): for a shared-row plan, the validation of every index
+ * (*err_word), each 8-query tile's row union and multiplicities and the
+ * longest-first tile order; for other plans nothing (their validation and
+ * compaction run inside the forward kernel). sa_forward with
+ * SA_FLAG_PLANNED and that workspace then starts at the attention kernel,
+ * so one plan serves every call that uses the same indices (for example
+ * layers that share a top-k selection).
+ * The plan depends on the values of topk_idxs and on b, m, kv_len, topk,
+ * the index strides, kv's row stride skv[1] and the other flags; q, kv's
+ * data, attn_sink, o and lse may differ between the calls. The forward
+ * only reads the workspace. No counterpart in the reference, which handles
+ * its indices inside each kernel call (track-01/submission.py:177-180,
+ * :313-322). Asynchronous; argument errors return before any device work.
+ */
+int sa_plan_indices(const sa_args* a, void* hip_stream);
 
 /* Kernels of one sa_forward call, in launch order. */
 enum {

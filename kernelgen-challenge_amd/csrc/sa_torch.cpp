@@ -1,7 +1,9 @@
 // sa_torch.cpp -- thin PyTorch-ROCm operator over the sparse_attn C-ABI.
 //
 // Registers torch.ops.sa_amd.sparse_attn_fwd (o), sparse_attn_fwd_lse
-// (o, lse) and sparse_attn_merge (o, lse of merged partials). They check
+// (o, lse), sparse_attn_merge (o, lse of merged partials), sparse_attn_plan
+// (the index plan of a topk_idxs tensor) and the planned forwards
+// sparse_attn_fwd_planned / sparse_attn_fwd_lse_planned. They check
 // devices and dtypes, allocate the outputs (like track-01/submission.py:1000)
 // and the workspace through the caching allocator, and call the C-ABI on the
 // current HIP stream. No kernel code lives here.
@@ -20,11 +22,14 @@ void check_rc(int rc, const char* what) {
 }
 
 // o, and lse when `want_lse` (fp32 [b, m, h]).
+// `plan`: the workspace of sparse_attn_plan for these indices (the forward
+// then skips the index kernels), or none.
 std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor& kv,
                                            const at::Tensor& attn_sink,
                                            const at::Tensor& topk_idxs, double scale,
                                            const c10::optional<at::Tensor>& err,
-                                           int64_t flags, bool want_lse) {
+                                           int64_t flags, bool want_lse,
+                                           const c10::optional<at::Tensor>& plan) {
   TORCH_CHECK_VALUE(q.dim() == 4, "q must be [b, m, h, d], got ", q.sizes());
   TORCH_CHECK_VALUE(kv.dim() == 3, "kv must be [b, kv_len, d], got ", kv.sizes());
   TORCH_CHECK_VALUE(attn_sink.dim() == 1, "attn_sink must be [h], got ",
@@ -68,7 +73,8 @@ std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor
   for (int i = 0; i < 3; ++i) a.sidx[i] = topk_idxs.stride(i);
   for (int i = 0; i < 4; ++i) a.so[i] = o.stride(i);
   a.scale = static_cast<float>(scale);
-  TORCH_CHECK_VALUE(flags >= 0 && flags <= 0xFFFFFFFFll, "bad flags ", flags);
+  TORCH_CHECK_VALUE(flags >= 0 && flags <= 0xFFFFFFFFll && (flags & SA_FLAG_PLANNED) == 0,
+                    "bad flags ", flags);
   a.flags = static_cast<uint32_t>(flags);
   if (err.has_value()) {
     TORCH_CHECK(err->device() == q.device() && err->scalar_type() == at::kInt &&
@@ -85,7 +91,15 @@ std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor
   size_t ws = 0;
   check_rc(sa_workspace_bytes(&a, &ws), "sparse_attn");
   at::Tensor workspace;
-  if (ws > 0) {
+  if (plan.has_value()) {
+    TORCH_CHECK_VALUE(plan->scalar_type() == at::kByte && plan->dim() == 1 &&
+                          plan->is_contiguous() && plan->device() == q.device() &&
+                          static_cast<size_t>(plan->numel()) >= ws,
+                      "plan is not an index plan of these arguments");
+    a.workspace = ws > 0 ? plan->data_ptr() : nullptr;
+    a.workspace_bytes = ws;
+    a.flags |= SA_FLAG_PLANNED;
+  } else if (ws > 0) {
     workspace = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
     a.workspace = workspace.data_ptr();
     a.workspace_bytes = ws;
@@ -94,17 +108,84 @@ std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor
   return {o, lse};
 }
 
+// The index plan of (q's shape, kv's length and row stride, topk_idxs): a
+// byte tensor holding the workspace that sa_plan_indices fills. q and kv are
+// read for their shapes and strides only.
+at::Tensor sparse_attn_plan(const at::Tensor& q, const at::Tensor& kv,
+                            const at::Tensor& topk_idxs, const c10::optional<at::Tensor>& err,
+                            int64_t flags) {
+  TORCH_CHECK_VALUE(q.dim() == 4 && kv.dim() == 3 && topk_idxs.dim() == 3,
+                    "expected q [b, m, h, d], kv [b, kv_len, d], topk_idxs [b, m, topk]");
+  TORCH_CHECK_TYPE(q.scalar_type() == at::kBFloat16 && kv.scalar_type() == at::kBFloat16,
+                   "q and kv must be bfloat16");
+  TORCH_CHECK_TYPE(topk_idxs.scalar_type() == at::kInt, "topk_idxs must be int32");
+  TORCH_CHECK(q.is_cuda() && kv.device() == q.device() && topk_idxs.device() == q.device(),
+              "all inputs must be on the same GPU");
+  TORCH_CHECK_VALUE(kv.size(0) == q.size(0) && topk_idxs.size(0) == q.size(0) &&
+                        topk_idxs.size(1) == q.size(1),
+                    "shapes of q ", q.sizes(), ", kv ", kv.sizes(), ", topk_idxs ",
+                    topk_idxs.sizes(), " do not match");
+  TORCH_CHECK_VALUE(flags >= 0 && flags <= 0xFFFFFFFFll && (flags & SA_FLAG_PLANNED) == 0,
+                    "bad flags ", flags);
+  const c10::DeviceGuard guard(q.device());
+  sa_args a{};
+  a.q = q.data_ptr();
+  a.kv = kv.data_ptr();
+  a.sink = static_cast<const float*>(q.data_ptr());  // not read by the index kernels
+  a.idx = topk_idxs.data_ptr<int32_t>();
+  a.o = q.data_ptr();                                 // not written by the index kernels
+  a.b = q.size(0);
+  a.m = q.size(1);
+  a.h = q.size(2);
+  a.d = q.size(3);
+  a.kv_len = kv.size(1);
+  a.topk = topk_idxs.size(2);
+  for (int i = 0; i < 4; ++i) a.sq[i] = q.stride(i);
+  for (int i = 0; i < 3; ++i) a.skv[i] = kv.stride(i);
+  for (int i = 0; i < 3; ++i) a.sidx[i] = topk_idxs.stride(i);
+  for (int i = 0; i < 4; ++i) a.so[i] = q.stride(i);
+  a.scale = 1.f;
+  a.flags = static_cast<uint32_t>(flags);
+  if (err.has_value()) {
+    TORCH_CHECK(err->device() == q.device() && err->scalar_type() == at::kInt &&
+                    err->numel() >= 1 && err->is_contiguous(),
+                "err must be a contiguous int32 tensor on q's device");
+    a.err_word = err->data_ptr<int32_t>();
+  }
+  size_t ws = 0;
+  check_rc(sa_workspace_bytes(&a, &ws), "sparse_attn_plan");
+  at::Tensor workspace = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
+  a.workspace = ws > 0 ? workspace.data_ptr() : nullptr;
+  a.workspace_bytes = ws;
+  check_rc(sa_plan_indices(&a, c10::hip::getCurrentHIPStream().stream()), "sparse_attn_plan");
+  return workspace;
+}
+
 at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
                            const at::Tensor& attn_sink, const at::Tensor& topk_idxs,
                            double scale, const c10::optional<at::Tensor>& err, int64_t flags) {
-  return std::get<0>(forward(q, kv, attn_sink, topk_idxs, scale, err, flags, false));
+  return std::get<0>(forward(q, kv, attn_sink, topk_idxs, scale, err, flags, false, {}));
+}
+
+at::Tensor sparse_attn_fwd_planned(const at::Tensor& q, const at::Tensor& kv,
+                                   const at::Tensor& attn_sink, const at::Tensor& topk_idxs,
+                                   double scale, const at::Tensor& plan,
+                                   const c10::optional<at::Tensor>& err, int64_t flags) {
+  return std::get<0>(forward(q, kv, attn_sink, topk_idxs, scale, err, flags, false, plan));
 }
 
 std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd_lse(
     const at::Tensor& q, const at::Tensor& kv, const at::Tensor& attn_sink,
     const at::Tensor& topk_idxs, double scale, const c10::optional<at::Tensor>& err,
     int64_t flags) {
-  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, true);
+  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, true, {});
+}
+
+std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd_lse_planned(
+    const at::Tensor& q, const at::Tensor& kv, const at::Tensor& attn_sink,
+    const at::Tensor& topk_idxs, double scale, const at::Tensor& plan,
+    const c10::optional<at::Tensor>& err, int64_t flags) {
+  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, true, plan);
 }
 
 // Merge n partials: o_parts bf16 [n, b, m, h, d], lse_parts fp32 [n, b, m, h].
@@ -167,10 +248,22 @@ TORCH_LIBRARY(sa_amd, m) {
       "float scale, Tensor? err=None, int flags=0) -> (Tensor, Tensor)");
   m.def("sparse_attn_merge(Tensor o_parts, Tensor lse_parts, Tensor? attn_sink=None) -> "
         "(Tensor, Tensor)");
+  m.def(
+      "sparse_attn_plan(Tensor q, Tensor kv, Tensor topk_idxs, Tensor? err=None, int flags=0) "
+      "-> Tensor");
+  m.def(
+      "sparse_attn_fwd_planned(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
+      "float scale, Tensor plan, Tensor? err=None, int flags=0) -> Tensor");
+  m.def(
+      "sparse_attn_fwd_lse_planned(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
+      "float scale, Tensor plan, Tensor? err=None, int flags=0) -> (Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
   m.impl("sparse_attn_fwd", &sparse_attn_fwd);
   m.impl("sparse_attn_fwd_lse", &sparse_attn_fwd_lse);
   m.impl("sparse_attn_merge", &sparse_attn_merge);
+  m.impl("sparse_attn_plan", &sparse_attn_plan);
+  m.impl("sparse_attn_fwd_planned", &sparse_attn_fwd_planned);
+  m.impl("sparse_attn_fwd_lse_planned", &sparse_attn_fwd_lse_planned);
 }

@@ -1393,7 +1393,10 @@ int current_cus(int* cus) {
   return SA_OK;
 }
 
-int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched);
+// What forward() launches: every kernel of a call, or only the index plan.
+enum class Launch { kCall, kPlanOnly };
+int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
+            Launch what = Launch::kCall);
 
 }  // namespace
 
@@ -1433,6 +1436,10 @@ int sa_forward_events(const sa_args* a, void* hip_stream, void* const* events,
                       uint32_t* launched) {
   if (launched != nullptr) *launched = 0u;
   return forward(a, static_cast<hipStream_t>(hip_stream), events, launched);
+}
+
+int sa_plan_indices(const sa_args* a, void* hip_stream) {
+  return forward(a, static_cast<hipStream_t>(hip_stream), nullptr, nullptr, Launch::kPlanOnly);
 }
 
 int sa_merge(const sa_merge_args* a, void* hip_stream) {
@@ -1476,7 +1483,10 @@ namespace {
 
 // The launches of one call. With `events`, records events[2k] / events[2k+1]
 // on the stream around kernel k (SA_KERNEL_*) and sets bit k of *launched.
-int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched) {
+// SA_FLAG_PLANNED skips the index kernels (their results are in the
+// workspace); Launch::kPlanOnly runs only them.
+int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
+            Launch what) {
   const int rc = sa::validate(a);
   if (rc != SA_OK) return rc;
   if (a->b == 0 || a->m == 0) return SA_OK;
@@ -1543,29 +1553,32 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     ip.force = (a->flags & SA_FLAG_FORCE_TILES) ? 1 : 0;
     ip.vec4 = ((reinterpret_cast<uintptr_t>(a->idx) & 15u) == 0 && a->topk % 4 == 0 &&
                a->sidx[0] % 4 == 0 && a->sidx[1] % 4 == 0) ? 1 : 0;
-    const size_t lds = size_t(a->kv_len) * sizeof(unsigned long long);
-    if (lds > 65536 &&
-        hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
-      return SA_EHIP;
-    if (!mark(SA_KERNEL_INDEX, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kIdxThreads), lds,
-                       stream, ip);
-    if (hipGetLastError() != hipSuccess) return SA_EHIP;
-    if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
     int32_t* order = reinterpret_cast<int32_t*>(ws + plan.order_off);
-    if (!mark(SA_KERNEL_ORDER, 0)) return SA_EHIP;
     int32_t* pq = reinterpret_cast<int32_t*>(ws + plan.pq_off);
-    OrderParams op{};
-    op.meta = ip.meta;
-    op.order = order;
-    op.pq = pq;
-    op.ntiles = int(plan.ntiles);
-    op.m = a->m;
-    op.tiles_per_b = plan.tiles_per_b;
-    hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, op);
-    if (hipGetLastError() != hipSuccess) return SA_EHIP;
-    if (!mark(SA_KERNEL_ORDER, 1)) return SA_EHIP;
+    if ((a->flags & SA_FLAG_PLANNED) == 0 || what == Launch::kPlanOnly) {
+      const size_t lds = size_t(a->kv_len) * sizeof(unsigned long long);
+      if (lds > 65536 &&
+          hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
+        return SA_EHIP;
+      if (!mark(SA_KERNEL_INDEX, 0)) return SA_EHIP;
+      hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kIdxThreads),
+                         lds, stream, ip);
+      if (hipGetLastError() != hipSuccess) return SA_EHIP;
+      if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
+      if (!mark(SA_KERNEL_ORDER, 0)) return SA_EHIP;
+      OrderParams op{};
+      op.meta = ip.meta;
+      op.order = order;
+      op.pq = pq;
+      op.ntiles = int(plan.ntiles);
+      op.m = a->m;
+      op.tiles_per_b = plan.tiles_per_b;
+      hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, op);
+      if (hipGetLastError() != hipSuccess) return SA_EHIP;
+      if (!mark(SA_KERNEL_ORDER, 1)) return SA_EHIP;
+    }
+    if (what == Launch::kPlanOnly) return SA_OK;
 
     TileParams tp{};
     tp.q = p.q;
@@ -1604,6 +1617,7 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     if (!mark(SA_KERNEL_TILE, 1)) return SA_EHIP;
     return SA_OK;
   }
+  if (what == Launch::kPlanOnly) return SA_OK;  // per-query plans keep no index state
 
   if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
   hipLaunchKernelGGL(sa_fwd_query_kernel, dim3(unsigned(p.nblocks)), dim3(kThreads), 0, stream, p);

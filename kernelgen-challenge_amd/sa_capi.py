@@ -17,7 +17,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libsparse_attn_gfx950.so")
 
 SA_OK, SA_EINVAL, SA_EUNSUPPORTED, SA_EWORKSPACE, SA_EHIP = range(5)
-SA_FLAG_PER_QUERY, SA_FLAG_FORCE_TILES = 1, 2
+SA_FLAG_PER_QUERY, SA_FLAG_FORCE_TILES, SA_FLAG_PLANNED = 1, 2, 4
 KERNELS = ("index", "order", "tile", "query", "combine")  # SA_KERNEL_* order
 SA_KERNEL_COUNT = len(KERNELS)
 
@@ -63,6 +63,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
                                       ctypes.POINTER(ctypes.c_void_p),
                                       ctypes.POINTER(ctypes.c_uint32)]
     lib.sa_merge.argtypes = [ctypes.POINTER(SaMergeArgs), ctypes.c_void_p]
+    lib.sa_plan_indices.argtypes = [args_p, ctypes.c_void_p]
     lib.sa_strerror.restype = ctypes.c_char_p
     lib.sa_strerror.argtypes = [ctypes.c_int]
     return lib

@@ -24,7 +24,8 @@ import threading
 
 import torch
 
-__all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "set_index_check", "index_check_enabled", "set_path_flags",
+__all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "sparse_attn_plan",
+           "IndexPlan", "set_index_check", "index_check_enabled", "set_path_flags",
            "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES"]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -36,7 +37,7 @@ _flags = 0
 
 # Kernel-path selection bits, as sa_args.flags in include/sparse_attn.h.
 FLAG_PER_QUERY = 1     # every query gathers its own rows
-FLAG_FORCE_TILES = 2   # every eligible 4-query tile shares its row union
+FLAG_FORCE_TILES = 2   # every eligible 8-query tile shares its row union
 
 
 def extension_path() -> str:
@@ -92,7 +93,65 @@ def _raise_if_bad_index(err, kv_len):
         raise RuntimeError(f"sparse_attn: topk_idxs holds an index outside [-1, {kv_len})")
 
 
-def sparse_attn(q, kv, attn_sink, topk_idxs, scale):
+class IndexPlan:
+    """The index preprocessing of ``sparse_attn`` for one ``topk_idxs`` tensor.
+
+    Made by :func:`sparse_attn_plan`; pass it as ``plan=`` to
+    :func:`sparse_attn` / :func:`sparse_attn_with_lse` to skip the
+    index-dependent kernels (validation, tile row unions, tile order) in every
+    call that uses the same indices, e.g. layers that share a top-k selection.
+    It holds the device workspace and the (contiguous) indices it was made
+    from. It is valid while ``topk_idxs`` is not modified in place (checked
+    through the tensor's version counter), for the same b, m, kv_len, topk,
+    kv row stride and path flags; q, kv's values and attn_sink may change.
+    Use it on the stream it was made on, or synchronize first.
+    """
+
+    __slots__ = ("workspace", "idx", "_src", "_src_ptr", "_src_version", "_key")
+
+    def __init__(self, workspace, idx, src, key):
+        self.workspace = workspace
+        self.idx = idx
+        self._src = src
+        self._src_ptr = src.data_ptr()
+        self._src_version = src._version
+        self._key = key
+
+    def _check(self, topk_idxs, key):
+        if (topk_idxs is not self._src and topk_idxs.data_ptr() != self._src_ptr) or \
+                topk_idxs._version != self._src_version:
+            raise ValueError("sparse_attn: plan was made for other (or since modified) topk_idxs")
+        if key != self._key:
+            raise ValueError("sparse_attn: plan was made for other shapes, strides or flags")
+
+
+def _plan_key(q, kv, topk_idxs):
+    return (tuple(q.shape), tuple(kv.shape), kv.stride(1), tuple(topk_idxs.shape), q.device,
+            _flags)
+
+
+def sparse_attn_plan(q, kv, topk_idxs):
+    """Index preprocessing of ``sparse_attn(q, kv, ., topk_idxs, .)`` on its own.
+
+    Returns an :class:`IndexPlan`. q and kv are used for their shapes and
+    kv's row stride only. With the index check on, an index outside
+    ``[-1, kv_len)`` raises here (for plans that keep index state) and in
+    the call.
+    """
+    if q.dim() != 4 or kv.dim() != 3 or topk_idxs.dim() != 3:
+        raise ValueError("expected q [b, m, h, d], kv [b, kv_len, d], topk_idxs [b, m, topk]")
+    if not (q.is_cuda and kv.is_cuda and topk_idxs.is_cuda):
+        raise ValueError("sparse_attn runs on the GPU only; move all inputs to the device")
+    load_extension()
+    idx_c = topk_idxs.contiguous()
+    kv_c = kv.contiguous()
+    err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
+    ws = torch.ops.sa_amd.sparse_attn_plan(q.contiguous(), kv_c, idx_c, err, _flags)
+    _raise_if_bad_index(err, kv.shape[1])
+    return IndexPlan(ws, idx_c, topk_idxs, _plan_key(q, kv_c, topk_idxs))
+
+
+def sparse_attn(q, kv, attn_sink, topk_idxs, scale, plan=None):
     """
     Args:
         q:          [b, m, h, d]   bf16   (h = 16, d = 512)
@@ -100,18 +159,25 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, scale):
         attn_sink:  [h]            fp32
         topk_idxs:  [b, m, topk]   int32  (-1 = padding slot)
         scale:      float
+        plan:       optional :class:`IndexPlan` of topk_idxs (this build
+                    only; the reference has no such argument)
 
     Returns:
         o:          [b, m, h, d]   bf16, a new tensor on q's device
     """
     q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
     err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
-    o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags)
+    if plan is None:
+        o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags)
+    else:
+        plan._check(topk_idxs, _plan_key(q, kv_c, topk_idxs))
+        o = torch.ops.sa_amd.sparse_attn_fwd_planned(q_c, kv_c, sink_c, plan.idx, float(scale),
+                                                     plan.workspace, err, _flags)
     _raise_if_bad_index(err, kv.shape[1])
     return o
 
 
-def sparse_attn_with_lse(q, kv, attn_sink, topk_idxs, scale):
+def sparse_attn_with_lse(q, kv, attn_sink, topk_idxs, scale, plan=None):
     """``sparse_attn`` that also returns the log-sum-exp of each (query, head).
 
     Returns ``(o, lse)``: ``o`` as ``sparse_attn``; ``lse`` fp32 ``[b, m, h]``,
@@ -120,11 +186,17 @@ def sparse_attn_with_lse(q, kv, attn_sink, topk_idxs, scale):
     ``o = sum_t exp(s_t - lse) * kv[idx_t]``. With ``attn_sink = -inf`` this is
     a partial result for :func:`sparse_attn_merge`. A query with no mass at
     all (no valid slot and sink = -inf) gets ``o = 0`` and ``lse = -inf``.
+    ``plan`` as in :func:`sparse_attn`.
     """
     q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
     err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
-    o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse(q_c, kv_c, sink_c, idx_c, float(scale),
-                                                  err, _flags)
+    if plan is None:
+        o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse(q_c, kv_c, sink_c, idx_c, float(scale),
+                                                      err, _flags)
+    else:
+        plan._check(topk_idxs, _plan_key(q, kv_c, topk_idxs))
+        o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse_planned(
+            q_c, kv_c, sink_c, plan.idx, float(scale), plan.workspace, err, _flags)
     _raise_if_bad_index(err, kv.shape[1])
     return o, lse
 

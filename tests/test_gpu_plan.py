@@ -1,0 +1,141 @@
+"""GPU tests of the index plan (sparse_attn_plan / sa_plan_indices +
+SA_FLAG_PLANNED): a planned call equals the unplanned call bit for bit on
+every plan kind, one plan serves calls with other q, kv values and sinks, and
+the Python layer refuses a plan whose indices changed."""
+import ctypes
+
+import pytest
+import torch
+
+from test_gpu_parity import DEV, sampled_check, say
+import sa_capi
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TILE, QUERY, INDEX, ORDER, COMBINE = 1 << 2, 1 << 3, 1 << 0, 1 << 1, 1 << 4
+
+
+def case(b, m, kv_len, topk, seed, minus1=0.0):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, m, 16, 512, generator=g).to(torch.bfloat16)
+    kv = torch.randn(b, kv_len, 512, generator=g).to(torch.bfloat16)
+    sink = torch.randn(16, generator=g)
+    idx = torch.randint(0, kv_len, (b, m, topk), generator=g, dtype=torch.int32)
+    if minus1:
+        idx[torch.rand(b, m, topk, generator=g) < minus1] = -1
+    return q.to(DEV), kv.to(DEV), sink.to(DEV), idx.to(DEV), wl.SCALE
+
+
+def windows(b, m, kv_len, seed):
+    """Overlapping windows: shared tiles (with b * m at least the 256 CUs of
+    an MI355X, so that no query is split and the plan has tiles)."""
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(b, m, 16, 512, generator=g).to(torch.bfloat16)
+    kv = torch.randn(b, kv_len, 512, generator=g).to(torch.bfloat16)
+    sink = torch.randn(16, generator=g)
+    idx = torch.stack([torch.arange(256, dtype=torch.int32) + 3 * t for t in range(m)])
+    idx = idx[None].repeat(b, 1, 1) % kv_len
+    idx[:, ::5, 200:] = -1
+    return q.to(DEV), kv.to(DEV), sink.to(DEV), idx.to(DEV), wl.SCALE
+
+
+CASES = {
+    "shared tiles": lambda: windows(2, 157, 3000, seed=1),
+    "per-query tiles": lambda: case(1, 300, 16384, 256, seed=2, minus1=0.1),
+    "split (decode)": lambda: case(8, 1, 32768, 2048, seed=3),
+    "per query, no split": lambda: case(1, 400, 20000, 128, seed=4, minus1=0.2),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_planned_equals_unplanned(gpu_sa, name):
+    q, kv, sink, idx, sc = CASES[name]()
+    plan = gpu_sa.sparse_attn_plan(q, kv, idx)
+    o0, l0 = gpu_sa.sparse_attn_with_lse(q, kv, sink, idx, sc)
+    for rep in range(2):
+        o1, l1 = gpu_sa.sparse_attn_with_lse(q, kv, sink, idx, sc, plan=plan)
+        assert torch.equal(o0, o1) and torch.equal(l0, l1)
+    assert torch.equal(gpu_sa.sparse_attn(q, kv, sink, idx, sc, plan=plan), o0)
+
+
+def test_plan_serves_other_values(gpu_sa):
+    """One plan, three calls with fresh q, kv values and sinks: each equals
+    its own unplanned call, and the oracle on sampled queries."""
+    q, kv, sink, idx, sc = windows(1, 300, 4096, seed=5)
+    plan = gpu_sa.sparse_attn_plan(q, kv, idx)
+    g = torch.Generator(device=DEV).manual_seed(6)
+    for rep in range(3):
+        q2 = torch.randn(q.shape, generator=g, device=DEV).to(torch.bfloat16)
+        kv2 = torch.randn(kv.shape, generator=g, device=DEV).to(torch.bfloat16)
+        s2 = torch.randn(16, generator=g, device=DEV) * 2
+        o_p = gpu_sa.sparse_attn(q2, kv2, s2, idx, sc, plan=plan)
+        o_u = gpu_sa.sparse_attn(q2, kv2, s2, idx, sc)
+        assert torch.equal(o_p, o_u)
+    sampled_check(o_p, q2.cpu(), kv2.cpu(), s2.cpu(), idx.cpu(), sc,
+                  [(0, t) for t in (0, 7, 8, 31, 299)], "planned")
+
+
+def test_plan_refuses_changed_indices(gpu_sa):
+    q, kv, sink, idx, sc = windows(1, 16, 1000, seed=7)
+    plan = gpu_sa.sparse_attn_plan(q, kv, idx)
+    with pytest.raises(ValueError):
+        gpu_sa.sparse_attn(q, kv, sink, idx.clone(), sc, plan=plan)      # other tensor
+    with pytest.raises(ValueError):
+        gpu_sa.sparse_attn(q[:, :8], kv, sink, idx[:, :8], sc, plan=plan)  # other shapes
+    idx[0, 0, 0] = 5                                                     # modified in place
+    with pytest.raises(ValueError):
+        gpu_sa.sparse_attn(q, kv, sink, idx, sc, plan=plan)
+    say("  stale plans refused")
+
+
+def test_plan_reports_bad_index(gpu_sa):
+    q, kv, sink, idx, sc = windows(1, 300, 1000, seed=8)   # a tile plan: checked there
+    idx[0, 3, 10] = 1000                                   # == kv_len: out of range
+    with pytest.raises(RuntimeError):
+        gpu_sa.sparse_attn_plan(q, kv, idx)
+
+
+def test_plan_of_an_aborting_tile(gpu_sa):
+    """A tile whose scores jump far above its reference runs per query inside
+    the shared-row kernel; planned, it does so again on every call."""
+    q, kv, sink, idx, sc = case(1, 256, 200, 128, seed=28)   # 256 queries: not split
+    kv[0, 150] = (q[0, 2].float().mean(0) * 60).to(torch.bfloat16)
+    idx[0, 2, :64] = torch.arange(64, dtype=torch.int32, device=DEV)
+    idx[0, 2, 64] = 150
+    gpu_sa.set_path_flags(gpu_sa.FLAG_FORCE_TILES)
+    try:
+        plan = gpu_sa.sparse_attn_plan(q, kv, idx)
+        o_u = gpu_sa.sparse_attn(q, kv, sink, idx, sc)
+        o_p = gpu_sa.sparse_attn(q, kv, sink, idx, sc, plan=plan)
+        o_p2 = gpu_sa.sparse_attn(q, kv, sink, idx, sc, plan=plan)
+    finally:
+        gpu_sa.set_path_flags(0)
+    assert torch.equal(o_u, o_p) and torch.equal(o_p, o_p2)
+
+
+@pytest.mark.parametrize("shape,plain,planned", [
+    ((1, 64, 300, 64), INDEX | ORDER | TILE, TILE),
+    ((4, 1, 2048, 512), QUERY | COMBINE, QUERY | COMBINE),
+    ((1, 3, 2048, 64), QUERY, QUERY),
+])
+def test_capi_planned_launches(gpu_sa, shape, plain, planned):
+    q, kv, sink, idx, sc = case(*shape, seed=sum(shape))
+    lib = sa_capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    o = torch.empty_like(q)
+    a = sa_capi.make_args(q, kv, sink, idx, o, sc)
+    n = sa_capi.workspace_bytes(lib, a)
+    ws = torch.empty(max(n, 1), dtype=torch.uint8, device=DEV)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), n
+    none = [None] * (2 * sa_capi.SA_KERNEL_COUNT)
+    assert sa_capi.forward_events(lib, a, stream, none) == plain
+    ref = o.clone()
+    o.fill_(float("nan"))
+    ws2 = torch.full((max(n, 1),), 0xAB, dtype=torch.uint8, device=DEV)  # a fresh workspace
+    a.workspace = ws2.data_ptr()
+    sa_capi.check(lib, lib.sa_plan_indices(ctypes.byref(a), ctypes.c_void_p(stream)), "plan")
+    a.flags = sa_capi.SA_FLAG_PLANNED
+    assert sa_capi.forward_events(lib, a, stream, none) == planned
+    torch.cuda.synchronize()
+    assert torch.equal(o, ref)

@@ -93,7 +93,9 @@ def test_tile_reference_jump_falls_back(gpu_sa):
     """A column whose scores jump far above its first step's max makes the tile
     hand itself to the per-query kernel (the tile kernel never rescales O):
     that tile's queries then match the per-query path bit for bit."""
-    q, kv, sink, idx, sc = rand_case(1, 16, 200, 128, seed=28)
+    # 256 queries (as many as CUs), so the plan does not split them and the
+    # tile path runs
+    q, kv, sink, idx, sc = rand_case(1, 256, 200, 128, seed=28)
     kv[0, 150] = (q[0, 2].float().mean(0) * 60).to(torch.bfloat16)  # a row matching query 2
     idx[0, 2, :64] = torch.arange(64, dtype=torch.int32)   # first step: ordinary rows
     idx[0, 2, 64] = 150                                     # later: a huge score

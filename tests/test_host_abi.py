@@ -97,7 +97,25 @@ def declared_functions():
 
 def test_header_declares_expected_api():
     assert declared_functions() == ["sa_abi_version", "sa_forward", "sa_forward_events",
-                                    "sa_merge", "sa_strerror", "sa_workspace_bytes"]
+                                    "sa_merge", "sa_plan_indices", "sa_strerror",
+                                    "sa_workspace_bytes"]
+
+
+def test_plan_indices_rejects_bad_args_without_device_work(libs):
+    hip, host = libs
+    hip.sa_plan_indices.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_void_p]
+    assert hip.sa_plan_indices(None, None) == SA_EINVAL
+    a = good_args()
+    a.d = 256
+    assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EUNSUPPORTED
+    a = good_args()
+    a.flags = 8
+    assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EINVAL
+    a = good_args(b=0)                         # empty: nothing to plan
+    assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_OK
+    a = good_args()
+    a.flags = 4                                # SA_FLAG_PLANNED is a valid bit
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_OK
 
 
 def test_ctypes_binding_matches_header_layout():
@@ -137,7 +155,7 @@ def test_library_exports_every_declared_symbol(libs):
     hip, _ = libs
     for name in declared_functions():
         assert hasattr(hip, name), f"{name} not exported"
-    assert hip.sa_abi_version() == 2
+    assert hip.sa_abi_version() == 3
 
 
 def test_strerror_covers_codes(libs):
@@ -162,7 +180,7 @@ def test_forward_rejects_null_args(libs):
     ("q", 0, SA_EINVAL), ("o", 0, SA_EINVAL), ("sink", 0, SA_EINVAL),
     ("idx", 0, SA_EINVAL), ("kv", 0, SA_EINVAL),
     ("q", 0x10008, SA_EINVAL), ("o", 0x50002, SA_EINVAL), ("kv", 0x20004, SA_EINVAL),
-    ("scale", float("nan"), SA_EINVAL), ("flags", 4, SA_EINVAL), ("flags", 1 << 31, SA_EINVAL),
+    ("scale", float("nan"), SA_EINVAL), ("flags", 8, SA_EINVAL), ("flags", 1 << 31, SA_EINVAL),
 ])
 def test_forward_argument_errors(libs, field, value, code):
     hip, host = libs
