@@ -958,19 +958,23 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
 
   const int qw = 2 * wave + (l32 >> 4);  // this lane's query within the tile
   const int hh = l32 & 15;                // and head
+  const uint32_t* urows = p.row_off + tile * p.cap;
+  // The first step's union offsets are loaded before Q: loads complete in
+  // order, so the first gather then waits for them alone, not for the
+  // 32 KiB of Q per wave, which arrives while the rows are gathered.
+  const int rows0 = int(urows[wave * kRowsPerWave + (lane & 15)]);
+  asm volatile("" ::: "memory");  // keep Q's loads after it
+  // Every lane loads (a lane past the tile's last query reads query 0 and
+  // zeroes it), so the loads are not under a branch and the first gather's
+  // wait counts only them as younger.
   bf16x8 qf[kDim / 16];
-  if (qw < qt) {
-    const __bf16* qrow = p.q + bi * p.sq_b + (q0 + qw) * p.sq_m + int64_t(hh) * p.sq_h + 8 * hi;
+  {
+    const __bf16* qrow = p.q + bi * p.sq_b + (q0 + (qw < qt ? qw : 0)) * p.sq_m +
+                         int64_t(hh) * p.sq_h + 8 * hi;
 #pragma unroll
     for (int s = 0; s < kDim / 16; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 16 * s);
-  } else {
-#pragma unroll
-    for (int s = 0; s < kDim / 16; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[s][e] = static_cast<__bf16>(0.f);
   }
 
-  const uint32_t* urows = p.row_off + tile * p.cap;
   const _Float16* ulc = p.lcnt + tile * p.cap * kTQ;
   const uint8_t* kvb = reinterpret_cast<const uint8_t*>(p.kv + bi * p.skv_b);
   // LDS address of this wave's first tile row in buffer 0
@@ -1004,11 +1008,14 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     asm volatile("" : "+a"(oacc[nb]));  // O lives in AGPRs (MFMA C/D only)
   }
 
-  {
-    const int rv = step_rows(0);
 #pragma unroll
-    for (int i = 0; i < kRowsPerWave; ++i) dma_row(rv, i, 0);
-    dma_counts(0, 0);
+  for (int i = 0; i < kRowsPerWave; ++i) dma_row(rows0, i, 0);
+  dma_counts(0, 0);
+  if (qw >= qt) {
+#pragma unroll
+    for (int s = 0; s < kDim / 16; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = static_cast<__bf16>(0.f);
   }
   int rows_next = step_rows(min(1, nsteps - 1));
   if (tid == 0) s_abort = 0;
