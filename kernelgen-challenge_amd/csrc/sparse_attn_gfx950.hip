@@ -47,6 +47,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "sa_plan.h"
 #include "sparse_attn.h"
 
@@ -453,19 +455,48 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
     for (int step = 0; step < nsteps; ++step) {
       wait_ring(min(nsteps - 1, step + kQAhead - 1) - step);
       lds_barrier();  // every wave's rows of `step` are in LDS; the previous buffer is free
-      if (step + kQAhead < nsteps) issue(step + kQAhead);
       const uint8_t* tb = sm.tile[step % kQRing];
+      // the list entries of the rows this wave gathers for step + kQAhead
+      const int sg = step + kQAhead;
+      int rv = 0;
+      if (sg < nsteps) {
+        const int e = sg * kQRows + wave * kQRowsPerWave + (lane & 7);
+        rv = s_list[e < nvalid ? e : 0];
+      }
+      const uint32_t lbase = lds_rows + uint32_t((sg % kQRing) * kQRows * kRowStride);
 
       // ---- S^T = K . Q^T for this wave's 8 rows ----------------------------------
-      // MFMA rows 8..15 repeat rows 0..7 (the A operand reads row n & 7).
+      // MFMA rows 8..15 repeat rows 0..7 (the A operand reads row n & 7). The K
+      // fragments are read 3 MFMAs ahead; the 8 row gathers of step +
+      // kQAhead ride between the MFMAs (one after every second), where their
+      // issue cost overlaps the MFMA chain.
       f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
       {
         const uint8_t* krow = tb + (wave * kQRowsPerWave + (n & 7)) * kRowStride + 16 * g;
+        auto s_chain = [&](auto with_dma) {
+          bf16x8 kf[4];
 #pragma unroll
-        for (int s = 0; s < kDim / 32; ++s) {
-          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(krow + 64 * s);
-          sacc = mfma_16x16x32(kf, qf[s], sacc);
-        }
+          for (int s = 0; s < 3; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 64 * s);
+#pragma unroll
+          for (int s = 0; s < kDim / 32; ++s) {
+            if (s + 3 < kDim / 32) kf[(s + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (s + 3));
+            sacc = mfma_16x16x32(kf[s & 3], qf[s], sacc);
+            if constexpr (decltype(with_dma)::value) {
+              if (s & 1) {
+                const int i = s >> 1;
+                const int row = __builtin_amdgcn_readlane(rv, i);
+                lds_dma_row(kvb + int64_t(row) * row_bytes, 16 * lane,
+                            lbase + uint32_t(i * kRowStride));
+              }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the interleave
+          }
+        };
+        static_assert(kDim / 32 == 2 * kQRowsPerWave, "one gather per two S^T MFMAs");
+        if (sg < nsteps)
+          s_chain(std::true_type{});
+        else
+          s_chain(std::false_type{});
       }
       // lane (n, g) now holds S[head n][row 8w + 4g + j], j = 0..3; lanes with
       // g >= 2 hold the repeated rows and drop them
