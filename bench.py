@@ -9,6 +9,11 @@ headline metric is quoted on. Calls rotate over ``--sets`` distinct input
 sets (separate q/kv/o buffers) so no call finds the previous call's data in
 the caches.
 
+Before the timed loops, untimed calls run for ``SETTLE_S`` seconds of wall
+time, because the W warmup calls of each loop are not enough on their own:
+the first ~10 ms of calls after the GPU was idle run up to 20 % slower while
+its clocks ramp. The count is reported as ``settle_calls``.
+
 Three timed loops of K calls each, all bracketed by ``torch.cuda.synchronize()``:
   1. whole calls through the drop-in (``submission.sparse_attn``), timed with
      HIP events on the stream the kernels run on -> ``value``, ``ms_per_step``;
@@ -84,6 +89,24 @@ def make_sets(name, nsets, dev):
         kvd = (torch.randn(kv.shape, generator=g, device=dev) * cfg.kv_std).to(torch.bfloat16)
         sets.append((qd, kvd, sets[0][2], sets[0][3].clone()))
     return cpu, sets
+
+
+SETTLE_S = 0.2
+
+
+def settle(fn, sets, scale, seconds=SETTLE_S):
+    """Untimed calls until `seconds` of wall time have passed (synchronizing
+    every 16 calls, so wall time is GPU time). Returns the number of calls."""
+    t0 = time.perf_counter()
+    n = 0
+    while time.perf_counter() - t0 < seconds:
+        s = sets[n % len(sets)]
+        fn(s[0], s[1], s[2], s[3], scale)
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    return n
 
 
 def time_calls(fn, sets, scale, steps, warmup, plans=None):
@@ -214,6 +237,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
     b, m = q.shape[0], q.shape[1]
     cfg = wl.CONFIGS[name]
     n_valid, flops, gathered, uniq, compulsory = algorithmic(idx, b, m)
+    settle_calls = settle(submission.sparse_attn, sets, scale)
     ms = time_calls(submission.sparse_attn, sets, scale, steps, warmup)
     times = kernel_times(sets, scale, steps, warmup)
     # the same calls with each input set's index plan made beforehand
@@ -231,6 +255,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
+        "settle_calls": settle_calls,
         "ms_per_step": round(ms, 5),
         "us_per_call": round(ms * 1e3, 2),
         "gathered_kv_GBps": round(gbps, 1),
