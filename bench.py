@@ -63,9 +63,9 @@ KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel"
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the same
 # counters read for a plain copy of known size (bench.py --copy-calibration:
 # FETCH_SIZE x 2.0000, WRITE_SIZE x 1.0000). Commands and raw figures:
-# profiles/sa_fwd_tile_kernel_causal_prefill_pmc_traffic.txt. Measured for
-# the kernels as built; a workload without an entry reports null.
-TRAFFIC = {"causal_prefill": 206151533}
+# profiles/<kernel>_<workload>_pmc.txt. Measured for the kernels as built.
+TRAFFIC = {"causal_prefill": 206045880, "high_locality": 387204574,
+           "long_context": 2125975845, "decode": 80157792, "plumbing": 17494614}
 
 
 def algorithmic(idx_cpu: torch.Tensor, b, m):
@@ -227,7 +227,7 @@ def roofline(name, flops, compulsory, times):
     return roof
 
 
-def bench_config(name, steps, warmup, nsets, with_cpu):
+def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     import submission
     submission.load_extension()
     submission.set_index_check(False)
@@ -237,7 +237,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu):
     b, m = q.shape[0], q.shape[1]
     cfg = wl.CONFIGS[name]
     n_valid, flops, gathered, uniq, compulsory = algorithmic(idx, b, m)
-    settle_calls = settle(submission.sparse_attn, sets, scale)
+    settle_calls = settle(submission.sparse_attn, sets, scale, settle_s)
     ms = time_calls(submission.sparse_attn, sets, scale, steps, warmup)
     times = kernel_times(sets, scale, steps, warmup)
     # the same calls with each input set's index plan made beforehand
@@ -305,6 +305,9 @@ def main():
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--all", action="store_true", help="also bench every config (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--settle", type=float, default=SETTLE_S,
+                    help="seconds of untimed calls before the timed loops (0 under a "
+                         "counter-collecting profiler, which serialises every dispatch)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy of known size (PMC byte scaling)")
     args = ap.parse_args()
@@ -322,10 +325,11 @@ def main():
         for name in wl.CONFIGS:
             if name == args.config:
                 continue
-            rec = bench_config(name, args.steps, args.warmup, args.sets, with_cpu=False)
+            rec = bench_config(name, args.steps, args.warmup, args.sets, with_cpu=False,
+                               settle_s=args.settle)
             print(json.dumps(rec), file=sys.stderr, flush=True)
     rec = bench_config(args.config, args.steps, args.warmup, args.sets,
-                       with_cpu=not args.no_cpu)
+                       with_cpu=not args.no_cpu, settle_s=args.settle)
     print(json.dumps(rec), flush=True)
 
 
