@@ -811,6 +811,12 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
 // The queries of per-query tiles go to the work list of the shared-row
 // kernel's per-query workers (pq[0] = count, pq[1] = number of shared tiles,
 // pq[2..] = flat query ids), in any order.
+// When the shared tiles fit the first wave of the shared-row kernel's grid
+// (at most one per CU, so every one starts at once) their order cannot
+// change when they finish; they are then placed for L2 reuse instead. Work-
+// group i runs on XCD i % 8, and XCD x gets the x-th eighth of the shared
+// tiles in tile order: consecutive queries of one batch, whose row unions
+// overlap and which sweep their ascending unions in step, share that XCD's L2.
 constexpr int kOrderThreads = 1024;
 constexpr int kOrderKeys = int(sa::kMaxTileKv / kTileRows) + 2;
 constexpr int kOrderKeysPadded = (kOrderKeys + 63) / 64 * 64;
@@ -822,17 +828,21 @@ static_assert(sa::kMaxUnits / (sa::kTileQueries / 2) <= (int64_t(1) << kOrderTil
               "tile ids fit the order entry");
 static_assert(kOrderKeys <= (1 << (31 - kOrderTileBits)), "keys fit the order entry");
 
+constexpr int kXcds = 8;  // MI355X: work-groups are dealt to the 8 XCDs round-robin
+
 struct OrderParams {
   const int32_t* meta;
   int32_t* order;
   int32_t* pq;
   int ntiles;
+  int cus;  // compute units of the device
   int64_t m, tiles_per_b;
 };
 
 __global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const OrderParams p) {
   __shared__ int s_pos[kOrderKeysPadded];
   __shared__ int s_npq;
+  __shared__ int s_wshared[kOrderThreads / 64];
   const int tid = threadIdx.x;
   const int32_t* meta = p.meta;
   const int ntiles = p.ntiles;
@@ -855,9 +865,37 @@ __global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const Orde
     }
   }
   __syncthreads();
+  const int nshared = ntiles - s_pos[0];  // shared tiles: every key above 0
   if (tid == 0) {
     p.pq[0] = s_npq;
-    p.pq[1] = ntiles - s_pos[0];  // shared tiles: every key above 0
+    p.pq[1] = nshared;
+  }
+  __syncthreads();  // every thread has read s_pos[0] before the scan rewrites it
+  if (nshared <= p.cus && ntiles <= kOrderThreads) {
+    // Every shared tile starts at once: XCD-local placement (see above). A
+    // tile's rank among the shared tiles in tile order picks its slot; the
+    // per-query tiles' entries fill the slots after them.
+    const bool sh = tid < ntiles && key(tid) > 0;
+    const unsigned long long bm = __ballot(sh);
+    if ((tid & 63) == 0) s_wshared[tid >> 6] = __popcll(bm);
+    __syncthreads();
+    int rank = __popcll(bm & ((1ull << (tid & 63)) - 1ull));
+    for (int w = 0; w < (tid >> 6); ++w) rank += s_wshared[w];
+    if (tid < ntiles) {
+      int slot = nshared + (tid - rank);  // a per-query tile: after the shared ones
+      if (sh) {
+        // XCD x holds the slots s < nshared with s % 8 == x: c_x of them
+        int first = 0, x = 0;
+        for (; x < kXcds - 1; ++x) {
+          const int c = (nshared - x + kXcds - 1) / kXcds;
+          if (rank < first + c) break;
+          first += c;
+        }
+        slot = kXcds * (rank - first) + x;
+      }
+      p.order[slot] = ((sh ? key(tid) : 0) << kOrderTileBits) | tid;
+    }
+    return;
   }
   if (tid < 64) {
     // exclusive scan over descending keys: the start of key k is the number
@@ -1612,6 +1650,7 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
       op.ntiles = int(plan.ntiles);
       op.m = a->m;
       op.tiles_per_b = plan.tiles_per_b;
+      op.cus = cus;
       hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, op);
       if (hipGetLastError() != hipSuccess) return SA_EHIP;
       if (!mark(SA_KERNEL_ORDER, 1)) return SA_EHIP;
