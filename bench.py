@@ -27,7 +27,15 @@ Three timed loops of K calls each, all bracketed by ``torch.cuda.synchronize()``
      a call whose indices are reused (not the headline ``value``).
 
 Printed: ONE JSON line (stdout). ``--all`` also prints one line per other
-configuration on stderr. ``--copy-calibration`` runs a plain device copy of
+configuration on stderr, and the track-02 lines below.
+
+``--sinkhorn`` instead times track 02's ``hc_split_sinkhorn`` on the
+reference's four serving scenarios (``track-02/workloads.py:19-24``): one JSON
+line per scenario with the decode and prefill µs/call on each lane layout and
+the automatic choice, the frequency-weighted latency the reference's bench
+reports (``track-02/bench.py:50-53``), the HBM roofline of the prefill call
+(96 bytes read and 96 written per token) and the NumPy float32 restatement
+timed on the host as the CPU baseline. ``--copy-calibration`` runs a plain device copy of
 known size instead (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters).
 """
 from __future__ import annotations
@@ -282,6 +290,102 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     return rec
 
 
+HC_WORKLOADS = [  # track-02/workloads.py:19-24: name, decode (b, s), share, prefill (b, s), share
+    ("16k-1k-1", (1, 1), 0.998, (1, 16384), 0.002),
+    ("4k-1k-16", (16, 1), 0.998, (16, 4096), 0.002),
+    ("1k-1k-64", (64, 1), 0.998, (64, 1024), 0.002),
+    ("1k-1-64", (64, 1), 0.333, (64, 1024), 0.672),
+]
+
+
+def bench_sinkhorn(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
+    """One record per track-02 scenario (see the module docstring)."""
+    from hc_sinkhorn import FLAG_LANES1, FLAG_LANES16, hc_split_sinkhorn
+    recs = []
+
+    def sets_for(b, s):
+        out = []
+        for i in range(nsets):
+            g = torch.Generator().manual_seed(500 + i)
+            out.append((torch.randn(b, s, 24, generator=g).cuda(),
+                        torch.randn(3, generator=g).cuda(), torch.randn(24, generator=g).cuda()))
+        return out
+
+    def us_per_call(sets, flags):
+        fn = lambda m, sc, bs: hc_split_sinkhorn(m, sc, bs, 4, 20, 1e-6, flags)
+        return time_calls(lambda m, sc, bs, _u, _s: fn(m, sc, bs),
+                          [(m, sc, bs, None) for m, sc, bs in sets], None, steps, warmup) * 1e3
+
+    import sa_capi
+    lib = sa_capi.hc_load()
+
+    def us_capi(sets):
+        """The C-ABI alone: outputs allocated once, one launch per call."""
+        stream = torch.cuda.current_stream()
+        outs = []
+        for m, sc, bs in sets:
+            n = m.numel() // 24
+            pre, post, comb = (torch.empty(n, 4, device=m.device), torch.empty(n, 4, device=m.device),
+                               torch.empty(n, 16, device=m.device))
+            outs.append((sa_capi.hc_make_args(m, sc, bs, pre, post, comb), (pre, post, comb)))
+        call = lambda i: sa_capi.check_hc(lib, lib.hc_split_sinkhorn(
+            ctypes.byref(outs[i % len(outs)][0]), ctypes.c_void_p(stream.cuda_stream)))
+        for i in range(warmup):
+            call(i)
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for i in range(steps):
+            call(i)
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) / steps * 1e3
+
+    first = True
+    for name, dshape, dshare, pshape, pshare in HC_WORKLOADS:
+        rec = {"op": "hc_split_sinkhorn", "scenario": name, "unit": "us/call",
+               "higher_is_better": False, "dtype": "f32", "data": "synthetic (seeded N(0,1))"}
+        for stage, shape in (("decode", dshape), ("prefill", pshape)):
+            sets = sets_for(*shape)
+            if first:
+                settle(lambda m, sc, bs, _u, _s: hc_split_sinkhorn(m, sc, bs),
+                       [(m, sc, bs, None) for m, sc, bs in sets], None, settle_s)
+                first = False
+            rec[stage] = {"shape": list(shape), "tokens": shape[0] * shape[1],
+                          "us_per_call": round(us_per_call(sets, 0), 2),
+                          "us_lanes16": round(us_per_call(sets, FLAG_LANES16), 2),
+                          "us_lanes1": round(us_per_call(sets, FLAG_LANES1), 2),
+                          "us_capi": round(us_capi(sets), 2)}
+        rec["weighted_us"] = round(dshare * rec["decode"]["us_per_call"] +
+                                   pshare * rec["prefill"]["us_per_call"], 3)
+        n = rec["prefill"]["tokens"]
+        hbm = n * 192 + 27 * 4
+        ach = hbm / (rec["prefill"]["us_per_call"] * 1e-6) / 1e9
+        rec["roofline_prefill"] = {"bound": "hbm", "traffic_alg": hbm, "achieved": round(ach, 1),
+                                   "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                                   "frac": round(ach / PEAK_HBM_GBPS, 4)}
+        if with_cpu:
+            from oracle.hc_sinkhorn_ref import hc_split_sinkhorn_np
+            cpu = {}
+            for stage, shape in (("decode", dshape), ("prefill", pshape)):
+                g = torch.Generator().manual_seed(900)
+                m = torch.randn(*shape, 24, generator=g).numpy()
+                sc = torch.randn(3, generator=g).numpy()
+                bs = torch.randn(24, generator=g).numpy()
+                hc_split_sinkhorn_np(m, sc, bs)
+                ts = []
+                for _ in range(3):
+                    t0 = time.perf_counter()
+                    hc_split_sinkhorn_np(m, sc, bs)
+                    ts.append(time.perf_counter() - t0)
+                cpu[stage] = round(statistics.median(ts) * 1e6, 1)
+            rec["cpu_baseline"] = {"decode_us": cpu["decode"], "prefill_us": cpu["prefill"],
+                                   "unit": "us/call", "cores": 1, "kind": "port",
+                                   "sample": "whole call, NumPy float32 restatement, median of 3"}
+        recs.append(rec)
+    return recs
+
+
 def copy_calibration(mib=1024, reps=5):
     """A plain device-to-device copy of `mib` MiB, `reps` times: under
     rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch scale the
@@ -308,6 +412,8 @@ def main():
     ap.add_argument("--settle", type=float, default=SETTLE_S,
                     help="seconds of untimed calls before the timed loops (0 under a "
                          "counter-collecting profiler, which serialises every dispatch)")
+    ap.add_argument("--sinkhorn", action="store_true",
+                    help="time track 02's hc_split_sinkhorn on its four scenarios instead")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy of known size (PMC byte scaling)")
     args = ap.parse_args()
@@ -321,7 +427,14 @@ def main():
     if args.copy_calibration:
         copy_calibration()
         return
+    if args.sinkhorn:
+        for rec in bench_sinkhorn(args.steps, args.warmup, args.sets, not args.no_cpu,
+                                  args.settle):
+            print(json.dumps(rec), flush=True)
+        return
     if args.all:
+        for rec in bench_sinkhorn(args.steps, args.warmup, args.sets, False, args.settle):
+            print(json.dumps(rec), file=sys.stderr, flush=True)
         for name in wl.CONFIGS:
             if name == args.config:
                 continue

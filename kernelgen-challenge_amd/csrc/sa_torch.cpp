@@ -3,15 +3,18 @@
 // Registers torch.ops.sa_amd.sparse_attn_fwd (o), sparse_attn_fwd_lse
 // (o, lse), sparse_attn_merge (o, lse of merged partials), sparse_attn_plan
 // (the index plan of a topk_idxs tensor) and the planned forwards
-// sparse_attn_fwd_planned / sparse_attn_fwd_lse_planned. They check
-// devices and dtypes, allocate the outputs (like track-01/submission.py:1000)
-// and the workspace through the caching allocator, and call the C-ABI on the
+// sparse_attn_fwd_planned / sparse_attn_fwd_lse_planned, and the track-02
+// operator hc_split_sinkhorn (pre, post, comb) over include/hc_sinkhorn.h.
+// They check devices and dtypes, allocate the outputs (like
+// track-01/submission.py:1000 and track-02/submission.py:353-355) and the
+// workspace through the caching allocator, and call the C-ABIs on the
 // current HIP stream. No kernel code lives here.
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
+#include "hc_sinkhorn.h"
 #include "sparse_attn.h"
 
 namespace {
@@ -237,6 +240,53 @@ std::tuple<at::Tensor, at::Tensor> sparse_attn_merge(const at::Tensor& o_parts,
   return {o, lse};
 }
 
+// track-02: mixes fp32 [b, s, 24], hc_scale fp32 [3], hc_base fp32 [24].
+// Returns pre [b, s, 4], post [b, s, 4], comb [b, s, 4, 4] (fp32).
+std::tuple<at::Tensor, at::Tensor, at::Tensor> hc_split_sinkhorn_op(
+    const at::Tensor& mixes, const at::Tensor& hc_scale, const at::Tensor& hc_base,
+    int64_t hc_mult, int64_t sinkhorn_iters, double eps, int64_t flags) {
+  TORCH_CHECK_VALUE(mixes.dim() == 3, "mixes must be 3-D [b, s, 24], got ", mixes.sizes());
+  TORCH_CHECK_VALUE(hc_mult == 4, "hc_split_sinkhorn is built for hc_mult = 4, got ", hc_mult);
+  TORCH_CHECK_VALUE(mixes.size(2) == 24, "mixes last dim must be 24, got ", mixes.size(2));
+  TORCH_CHECK_VALUE(hc_scale.numel() == 3 && hc_base.numel() == 24,
+                    "hc_scale must have 3 and hc_base 24 elements");
+  for (const at::Tensor* t : {&mixes, &hc_scale, &hc_base})
+    TORCH_CHECK_TYPE(t->scalar_type() == at::kFloat, "mixes, hc_scale and hc_base must be float32");
+  TORCH_CHECK(mixes.is_cuda() && hc_scale.device() == mixes.device() &&
+                  hc_base.device() == mixes.device(),
+              "mixes, hc_scale and hc_base must be on the same GPU");
+  TORCH_CHECK_VALUE(sinkhorn_iters >= INT32_MIN && sinkhorn_iters <= INT32_MAX,
+                    "sinkhorn_iters out of range");
+  const c10::DeviceGuard guard(mixes.device());
+  at::Tensor x = mixes.contiguous();
+  if ((reinterpret_cast<uintptr_t>(x.data_ptr()) & 15u) != 0) x = x.clone();  // 16-byte rows
+  const at::Tensor sc = hc_scale.contiguous();
+  const at::Tensor bs = hc_base.contiguous();
+  const int64_t b = mixes.size(0), s = mixes.size(1), n = b * s;
+  // One allocation, three contiguous outputs carved from it (pre, post, comb)
+  at::Tensor out = at::empty({24 * n}, x.options());
+  at::Tensor pre = out.narrow(0, 0, 4 * n).view({b, s, 4});
+  at::Tensor post = out.narrow(0, 4 * n, 4 * n).view({b, s, 4});
+  at::Tensor comb = out.narrow(0, 8 * n, 16 * n).view({b, s, 4, 4});
+  hc_args a{};
+  a.mixes = x.data_ptr<float>();
+  a.scale = sc.data_ptr<float>();
+  a.base = bs.data_ptr<float>();
+  a.pre = pre.data_ptr<float>();
+  a.post = post.data_ptr<float>();
+  a.comb = comb.data_ptr<float>();
+  a.n = n;
+  a.hc_mult = int32_t(hc_mult);
+  a.iters = int32_t(sinkhorn_iters);
+  a.eps = float(eps);
+  a.flags = uint32_t(flags);
+  const int rc = hc_split_sinkhorn(&a, c10::hip::getCurrentHIPStream().stream());
+  TORCH_CHECK_VALUE(rc != HC_EINVAL && rc != HC_EUNSUPPORTED, "hc_split_sinkhorn: ",
+                    hc_strerror(rc));
+  TORCH_CHECK(rc == HC_OK, "hc_split_sinkhorn: ", hc_strerror(rc));
+  return {pre, post, comb};
+}
+
 }  // namespace
 
 TORCH_LIBRARY(sa_amd, m) {
@@ -257,6 +307,9 @@ TORCH_LIBRARY(sa_amd, m) {
   m.def(
       "sparse_attn_fwd_lse_planned(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
       "float scale, Tensor plan, Tensor? err=None, int flags=0) -> (Tensor, Tensor)");
+  m.def(
+      "hc_split_sinkhorn(Tensor mixes, Tensor hc_scale, Tensor hc_base, int hc_mult=4, "
+      "int sinkhorn_iters=20, float eps=1e-6, int flags=0) -> (Tensor, Tensor, Tensor)");
 }
 
 TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
@@ -266,4 +319,5 @@ TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
   m.impl("sparse_attn_plan", &sparse_attn_plan);
   m.impl("sparse_attn_fwd_planned", &sparse_attn_fwd_planned);
   m.impl("sparse_attn_fwd_lse_planned", &sparse_attn_fwd_lse_planned);
+  m.impl("hc_split_sinkhorn", &hc_split_sinkhorn_op);
 }

@@ -110,3 +110,51 @@ def forward_events(lib: ctypes.CDLL, a: SaArgs, stream: int, events) -> int:
     check(lib, lib.sa_forward_events(ctypes.byref(a), ctypes.c_void_p(stream), handles,
                                      ctypes.byref(launched)), "sa_forward_events")
     return launched.value
+
+
+# ---------------------------------------------------------------------------
+# track-02 hc_split_sinkhorn (include/hc_sinkhorn.h)
+# ---------------------------------------------------------------------------
+HC_LIB_PATH = os.path.join(_HERE, "lib", "libhc_sinkhorn_gfx950.so")
+HC_OK, HC_EINVAL, HC_EUNSUPPORTED, HC_EHIP = range(4)
+HC_FLAG_LANES16, HC_FLAG_LANES1 = 1, 2
+
+
+class HcArgs(ctypes.Structure):
+    """``struct hc_args`` (include/hc_sinkhorn.h)."""
+    _fields_ = [
+        ("mixes", ctypes.c_void_p), ("scale", ctypes.c_void_p), ("base", ctypes.c_void_p),
+        ("pre", ctypes.c_void_p), ("post", ctypes.c_void_p), ("comb", ctypes.c_void_p),
+        ("n", ctypes.c_int64), ("hc_mult", ctypes.c_int32), ("iters", ctypes.c_int32),
+        ("eps", ctypes.c_float), ("flags", ctypes.c_uint32),
+    ]
+
+
+def hc_load(path: str = HC_LIB_PATH) -> ctypes.CDLL:
+    """Load the track-02 library and declare its entry points."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    lib.hc_abi_version.restype = ctypes.c_int
+    lib.hc_abi_version.argtypes = []
+    lib.hc_strerror.restype = ctypes.c_char_p
+    lib.hc_strerror.argtypes = [ctypes.c_int]
+    lib.hc_split_sinkhorn.argtypes = [ctypes.POINTER(HcArgs), ctypes.c_void_p]
+    return lib
+
+
+def check_hc(lib, rc: int, what: str = "hc_split_sinkhorn") -> None:
+    if rc != HC_OK:
+        raise RuntimeError(f"{what}: {lib.hc_strerror(rc).decode()} (code {rc})")
+
+
+def hc_make_args(mixes, scale, base, pre, post, comb, iters=20, eps=1e-6, flags=0,
+                 hc_mult=4) -> HcArgs:
+    """hc_args for contiguous fp32 torch tensors mixes [..., 24], scale [3],
+    base [24], pre / post [..., 4], comb [..., 4, 4]."""
+    a = HcArgs()
+    a.mixes, a.scale, a.base = mixes.data_ptr(), scale.data_ptr(), base.data_ptr()
+    a.pre, a.post, a.comb = pre.data_ptr(), post.data_ptr(), comb.data_ptr()
+    a.n = mixes.numel() // 24
+    a.hc_mult, a.iters, a.eps, a.flags = hc_mult, iters, eps, flags
+    return a

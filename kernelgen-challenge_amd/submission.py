@@ -26,7 +26,8 @@ import torch
 
 __all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "sparse_attn_plan",
            "IndexPlan", "set_index_check", "index_check_enabled", "set_path_flags",
-           "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES"]
+           "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES",
+           "hc_split_sinkhorn"]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 _EXT_PATH = os.path.join(_PKG_DIR, "lib", "sa_torch_ext.so")
@@ -226,3 +227,8 @@ def sparse_attn_merge(o_parts, lse_parts, attn_sink=None):
         raise ValueError("sparse_attn_merge runs on the GPU only")
     load_extension()
     return torch.ops.sa_amd.sparse_attn_merge(o_parts, lse_parts, attn_sink)
+
+
+# Track 02's entry point, so that ``from submission import hc_split_sinkhorn``
+# (track-02/test_correctness.py:14, bench.py:14) finds it here as well.
+from hc_sinkhorn import hc_split_sinkhorn  # noqa: E402
