@@ -72,8 +72,8 @@ KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel"
 # counters read for a plain copy of known size (bench.py --copy-calibration:
 # FETCH_SIZE x 2.0000, WRITE_SIZE x 1.0000). Commands and raw figures:
 # profiles/<kernel>_<workload>_pmc.txt. Measured for the kernels as built.
-TRAFFIC = {"causal_prefill": 206045880, "high_locality": 387204574,
-           "long_context": 2125975845, "decode": 80157792, "plumbing": 17494614}
+TRAFFIC = {"causal_prefill": 206198454, "high_locality": 232269823,
+           "long_context": 2125966694, "decode": 80157116, "plumbing": 17494372}
 
 
 def algorithmic(idx_cpu: torch.Tensor, b, m):
