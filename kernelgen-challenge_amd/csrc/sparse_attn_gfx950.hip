@@ -371,17 +371,6 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
   const int64_t s_begin = int64_t(split) * p.split_len;
   const int64_t s_end = min(p.topk, s_begin + p.split_len);
 
-  // Q^T as the B operand of S^T = K . Q^T: lane (n, g) holds head n,
-  // d = 32s + 8g .. 32s + 8g + 7 for k-step s. Issued first, so the
-  // compaction's wait for the indices covers it.
-  bf16x8 qf[kDim / 32];
-  {
-    const __bf16* qrow = p.q + bi * p.sq_b + mi * p.sq_m + int64_t(n) * p.sq_h + 8 * g;
-#pragma unroll
-    for (int s = 0; s < kDim / 32; ++s)
-      qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
-  }
-
   const uint8_t* kvb = reinterpret_cast<const uint8_t*>(p.kv + bi * p.skv_b);
   const int64_t row_bytes = p.skv_n * 2;
   const int32_t* irow = p.idx + bi * p.si_b + mi * p.si_m;
@@ -395,6 +384,7 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
 #pragma unroll
   for (int i = 0; i < kDBlocks; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  bf16x8 qf[kDim / 32];
   for (int64_t base = s_begin; base < s_end; base += kListCap) {
     const int cnt = int(min(int64_t(kListCap), s_end - base));
     __syncthreads();  // the previous batch is done with s_list and the ring
@@ -402,11 +392,27 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
     int vals[kSlotsPerThread];
     int c = 0;
     bool bad = false;
+    int raw[kSlotsPerThread];
 #pragma unroll
     for (int i = 0; i < kSlotsPerThread; ++i) {
       const int sl = tid * kSlotsPerThread + i;
-      int v = -1;
-      if (sl < cnt) v = irow[base + sl];
+      raw[i] = sl < cnt ? irow[base + sl] : -1;
+    }
+    {
+      // Q^T as the B operand of S^T = K . Q^T: lane (n, g) holds head n,
+      // d = 32s + 8g .. 32s + 8g + 7 for k-step s. Issued after the index
+      // loads (which return first, so the compaction waits for them alone)
+      // and complete before the first gather is issued (vmcnt below). Not
+      // under a branch, so that the compiler's wait for the indices counts
+      // these loads as younger; a batch after the first reloads the same Q.
+      const __bf16* qrow = p.q + bi * p.sq_b + mi * p.sq_m + int64_t(n) * p.sq_h + 8 * g;
+#pragma unroll
+      for (int s = 0; s < kDim / 32; ++s)
+        qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+    }
+#pragma unroll
+    for (int i = 0; i < kSlotsPerThread; ++i) {
+      const int v = raw[i];
       const bool ok = (v >= 0) && (int64_t(v) < p.kv_len);
       bad |= (!ok && v != -1);
       vals[i] = ok ? v : -1;
@@ -435,6 +441,9 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
     __syncthreads();
     if (nvalid == 0) continue;
     const int nsteps = (nvalid + kQRows - 1) / kQRows;
+    // every load of this wave (Q) is complete before the gathers, whose
+    // ring waits count only them
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
     // ---- gather ring -----------------------------------------------------------
     // Wave w gathers rows 8w..8w+7 of a step; lane i < 8 reads the list entry
