@@ -160,3 +160,16 @@ def test_capi_direct(flags):
     ref = hc_split_sinkhorn(md, sd, bd, flags=flags)
     for x, y in zip(ref, (pre, post, comb)):
         assert torch.equal(x, y)
+
+
+def test_rejects_wrong_dtype_and_device():
+    say("hc_split_sinkhorn argument errors")
+    mixes, sc, base = [t.to(DEV) for t in make(2, 3, seed=2)]
+    with pytest.raises(TypeError, match="float32"):
+        hc_split_sinkhorn(mixes.double(), sc, base)
+    with pytest.raises(TypeError, match="float32"):
+        hc_split_sinkhorn(mixes.to(torch.bfloat16), sc, base)
+    with pytest.raises(ValueError, match="3 and hc_base 24"):
+        hc_split_sinkhorn(mixes, sc[:2], base)
+    with pytest.raises(ValueError, match="GPU only"):
+        hc_split_sinkhorn(mixes, sc.cpu(), base)
