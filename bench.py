@@ -56,7 +56,7 @@ for _p in (REPO, PKG):
 
 import torch  # noqa: E402
 
-import workloads as wl  # noqa: E402
+import sa_workloads as wl  # noqa: E402
 
 METRIC = ("sparse_attn µs/call, TFLOP/s + gathered-KV GB/s (% roofline) "
           "at m4096 topk2048")
@@ -238,7 +238,7 @@ def roofline(name, flops, compulsory, times):
 def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     import submission
     submission.load_extension()
-    submission.set_index_check(False)
+    submission.set_index_check("deferred")  # the drop-in's default mode
     dev = "cuda"
     cpu_inputs, sets = make_sets(name, nsets, dev)
     q, kv, sink, idx, scale = cpu_inputs

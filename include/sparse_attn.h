@@ -18,7 +18,7 @@
  *                      all -1 yields o = 0 (the sink takes all the mass).
  *   0 .. kv_len-1      valid; duplicates count with multiplicity.
  *   anything else      out of range: the slot is excluded, never read, and
- *                      *err_word (if non-null) gets bit 0 set. The reference
+ *                      1 is stored into *err_word (if non-null). The reference
  *                      raises here (torch.gather at reference.py:28); the
  *                      Python layer turns the flag into RuntimeError.
  *
@@ -79,7 +79,10 @@ typedef struct sa_args {
   float scale;            /* softmax scale, e.g. d**-0.5 */
   void* workspace;        /* device scratch: tile row unions, split partials */
   size_t workspace_bytes;
-  int32_t* err_word;      /* device int32, nullable; bit 0 = bad index seen */
+  int32_t* err_word;      /* int32, nullable; set to 1 when a bad index is seen
+                             (a system-scope store, never cleared by the library:
+                             device memory, or mapped pinned host memory that the
+                             host reads without synchronizing) */
   uint32_t flags;         /* SA_FLAG_* bits, normally 0 */
   float* lse;             /* fp32 [b, m, h], nullable: log-sum-exp per (query, head) */
   int64_t slse[3];        /* strides of lse */

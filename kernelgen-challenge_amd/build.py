@@ -49,7 +49,10 @@ HIP_FLAGS = [
 ]
 
 
-def _run(cmd, verbose):
+def _run(cmd, verbose, strict=False):
+    """Run one compiler command. Its diagnostics are always printed (hipcc's
+    host-pass note that it does not know the packed-fp32 feature aside, which
+    is harmless); with ``strict`` any of them fails the build."""
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -58,8 +61,10 @@ def _run(cmd, verbose):
         raise RuntimeError(f"build step failed ({res.returncode}): {cmd[0]} ... {cmd[-1]}")
     noise = [ln for ln in (res.stdout + res.stderr).splitlines()
              if ln.strip() and "packed-fp32-ops" not in ln]
-    if verbose and noise:
-        print("\n".join(noise))
+    if noise:
+        sys.stderr.write("\n".join(noise) + "\n")
+        if strict:
+            raise RuntimeError(f"build step printed diagnostics (treated as errors): {cmd[-3]}")
 
 
 def _atomic_target(path):
@@ -71,7 +76,7 @@ def build_hip_lib(verbose=False):
     for src, out in (("sparse_attn_gfx950.hip", HIP_LIB), ("hc_sinkhorn_gfx950.hip", HC_LIB)):
         tmp = _atomic_target(out)
         _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}",
-              os.path.join(CSRC, src), "-o", tmp], verbose)
+              os.path.join(CSRC, src), "-o", tmp], verbose, strict=True)
         os.replace(tmp, out)
 
 

@@ -20,6 +20,9 @@ constexpr int64_t kMaxUnits = int64_t(1) << 24;  // work-groups per launch
 // LDS (one byte per query, 8 bytes per row), so it needs kv_len <= kMaxTileKv.
 constexpr int kTileQueries = 8;
 constexpr int64_t kMaxTileKv = 16384;
+// The index kernel counts a tile's slots (kTileQueries * topk, plus one round
+// of loads past the end) in 32-bit integers: tiles need topk <= 2^27.
+constexpr int64_t kMaxTileTopk = int64_t(1) << 27;
 
 // Tile modes written by the index kernel.
 constexpr int kModePerQuery = 0;
@@ -133,7 +136,8 @@ inline int validate_merge(const sa_merge_args* a) {
 // compute units, and never into parts shorter than one pipeline tile, so
 // decode shapes (few queries, long topk) still occupy every CU. Shared-row
 // tiles are planned when every query has its own work-group (no split), the
-// batch has at least one full tile and the count table fits in LDS.
+// batch has at least half a tile, the count table fits in LDS and the tile's
+// slot count fits 32 bits.
 inline Plan make_plan(const sa_args* a, int num_cus) {
   Plan p{};
   p.units = a->b * a->m;
@@ -160,8 +164,8 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
   const bool offsets32 =
       a->kv_len > 0 && (a->kv_len - 1) * a->skv[1] * 2 + 2 * kDim <= int64_t(UINT32_MAX);
   p.tiles = p.nsplit == 1 && (a->flags & SA_FLAG_PER_QUERY) == 0 &&
-            a->m >= kTileQueries / 2 && a->topk > 0 && a->kv_len > 0 &&
-            a->kv_len <= kMaxTileKv && offsets32;
+            a->m >= kTileQueries / 2 && a->topk > 0 && a->topk <= kMaxTileTopk &&
+            a->kv_len > 0 && a->kv_len <= kMaxTileKv && offsets32;
   size_t off = 0;
   if (p.tiles) {
     p.tiles_per_b = (a->m + kTileQueries - 1) / kTileQueries;

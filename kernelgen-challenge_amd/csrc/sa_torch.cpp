@@ -12,7 +12,10 @@
 #include <ATen/ATen.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
 #include <torch/library.h>
+
+#include <mutex>
 
 #include "hc_sinkhorn.h"
 #include "sparse_attn.h"
@@ -24,6 +27,58 @@ void check_rc(int rc, const char* what) {
   TORCH_CHECK(rc == SA_OK, what, ": ", sa_strerror(rc));
 }
 
+// Deferred index check: one int32 per device in mapped pinned host memory,
+// passed to the kernels as sa_args.err_word. A kernel that meets an index
+// outside [-1, kv_len) stores 1 into it; the host reads it with a plain load,
+// so a call never waits for the GPU to learn of an earlier call's bad index.
+// Allocated on first use and kept until the process ends.
+constexpr int kMaxFlagDevices = 64;
+struct HostFlag {
+  int32_t* host = nullptr;  // host address (read / cleared by Python)
+  int32_t* dev = nullptr;   // the same word as the GPU addresses it
+};
+std::mutex g_flag_mu;
+HostFlag g_flags[kMaxFlagDevices];
+
+HostFlag host_flag(int device) {
+  TORCH_CHECK(device >= 0 && device < kMaxFlagDevices, "device index ", device, " out of range");
+  std::lock_guard<std::mutex> lock(g_flag_mu);
+  HostFlag& f = g_flags[device];
+  if (f.host == nullptr) {
+    const c10::DeviceGuard guard(c10::Device(c10::DeviceType::CUDA, device));
+    void* h = nullptr;
+    TORCH_CHECK(hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocPortable) == hipSuccess,
+                "sparse_attn: hipHostMalloc of the index-error flag failed");
+    void* d = nullptr;
+    if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+      (void)hipHostFree(h);
+      TORCH_CHECK(false, "sparse_attn: hipHostGetDevicePointer of the index-error flag failed");
+    }
+    *static_cast<volatile int32_t*>(h) = 0;
+    f.host = static_cast<int32_t*>(h);
+    f.dev = static_cast<int32_t*>(d);
+  }
+  return f;
+}
+
+// Host address of the device's deferred index-error flag (an int32).
+int64_t index_error_flag_address(int64_t device) {
+  return static_cast<int64_t>(reinterpret_cast<uintptr_t>(host_flag(int(device)).host));
+}
+
+// err_word of a call: the caller's device tensor, else the deferred flag when
+// asked for, else none.
+int32_t* err_word(const c10::optional<at::Tensor>& err, bool deferred_check,
+                  const at::Device& dev) {
+  if (err.has_value()) {
+    TORCH_CHECK(err->device() == dev && err->scalar_type() == at::kInt &&
+                    err->numel() >= 1 && err->is_contiguous(),
+                "err must be a contiguous int32 tensor on q's device");
+    return err->data_ptr<int32_t>();
+  }
+  return deferred_check ? host_flag(dev.index()).dev : nullptr;
+}
+
 // o, and lse when `want_lse` (fp32 [b, m, h]).
 // `plan`: the workspace of sparse_attn_plan for these indices (the forward
 // then skips the index kernels), or none.
@@ -31,7 +86,7 @@ std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor
                                            const at::Tensor& attn_sink,
                                            const at::Tensor& topk_idxs, double scale,
                                            const c10::optional<at::Tensor>& err,
-                                           int64_t flags, bool want_lse,
+                                           int64_t flags, bool deferred_check, bool want_lse,
                                            const c10::optional<at::Tensor>& plan) {
   TORCH_CHECK_VALUE(q.dim() == 4, "q must be [b, m, h, d], got ", q.sizes());
   TORCH_CHECK_VALUE(kv.dim() == 3, "kv must be [b, kv_len, d], got ", kv.sizes());
@@ -79,12 +134,7 @@ std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor
   TORCH_CHECK_VALUE(flags >= 0 && flags <= 0xFFFFFFFFll && (flags & SA_FLAG_PLANNED) == 0,
                     "bad flags ", flags);
   a.flags = static_cast<uint32_t>(flags);
-  if (err.has_value()) {
-    TORCH_CHECK(err->device() == q.device() && err->scalar_type() == at::kInt &&
-                    err->numel() >= 1 && err->is_contiguous(),
-                "err must be a contiguous int32 tensor on q's device");
-    a.err_word = err->data_ptr<int32_t>();
-  }
+  a.err_word = err_word(err, deferred_check, q.device());
   if (want_lse) {
     lse = at::empty({b, m, h}, q.options().dtype(at::kFloat));
     a.lse = lse.data_ptr<float>();
@@ -116,7 +166,7 @@ std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor
 // read for their shapes and strides only.
 at::Tensor sparse_attn_plan(const at::Tensor& q, const at::Tensor& kv,
                             const at::Tensor& topk_idxs, const c10::optional<at::Tensor>& err,
-                            int64_t flags) {
+                            int64_t flags, bool deferred_check) {
   TORCH_CHECK_VALUE(q.dim() == 4 && kv.dim() == 3 && topk_idxs.dim() == 3,
                     "expected q [b, m, h, d], kv [b, kv_len, d], topk_idxs [b, m, topk]");
   TORCH_CHECK_TYPE(q.scalar_type() == at::kBFloat16 && kv.scalar_type() == at::kBFloat16,
@@ -149,12 +199,7 @@ at::Tensor sparse_attn_plan(const at::Tensor& q, const at::Tensor& kv,
   for (int i = 0; i < 4; ++i) a.so[i] = q.stride(i);
   a.scale = 1.f;
   a.flags = static_cast<uint32_t>(flags);
-  if (err.has_value()) {
-    TORCH_CHECK(err->device() == q.device() && err->scalar_type() == at::kInt &&
-                    err->numel() >= 1 && err->is_contiguous(),
-                "err must be a contiguous int32 tensor on q's device");
-    a.err_word = err->data_ptr<int32_t>();
-  }
+  a.err_word = err_word(err, deferred_check, q.device());
   size_t ws = 0;
   check_rc(sa_workspace_bytes(&a, &ws), "sparse_attn_plan");
   at::Tensor workspace = at::empty({static_cast<int64_t>(ws)}, q.options().dtype(at::kByte));
@@ -166,29 +211,33 @@ at::Tensor sparse_attn_plan(const at::Tensor& q, const at::Tensor& kv,
 
 at::Tensor sparse_attn_fwd(const at::Tensor& q, const at::Tensor& kv,
                            const at::Tensor& attn_sink, const at::Tensor& topk_idxs,
-                           double scale, const c10::optional<at::Tensor>& err, int64_t flags) {
-  return std::get<0>(forward(q, kv, attn_sink, topk_idxs, scale, err, flags, false, {}));
+                           double scale, const c10::optional<at::Tensor>& err, int64_t flags,
+                           bool deferred_check) {
+  return std::get<0>(
+      forward(q, kv, attn_sink, topk_idxs, scale, err, flags, deferred_check, false, {}));
 }
 
 at::Tensor sparse_attn_fwd_planned(const at::Tensor& q, const at::Tensor& kv,
                                    const at::Tensor& attn_sink, const at::Tensor& topk_idxs,
                                    double scale, const at::Tensor& plan,
-                                   const c10::optional<at::Tensor>& err, int64_t flags) {
-  return std::get<0>(forward(q, kv, attn_sink, topk_idxs, scale, err, flags, false, plan));
+                                   const c10::optional<at::Tensor>& err, int64_t flags,
+                                   bool deferred_check) {
+  return std::get<0>(
+      forward(q, kv, attn_sink, topk_idxs, scale, err, flags, deferred_check, false, plan));
 }
 
 std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd_lse(
     const at::Tensor& q, const at::Tensor& kv, const at::Tensor& attn_sink,
     const at::Tensor& topk_idxs, double scale, const c10::optional<at::Tensor>& err,
-    int64_t flags) {
-  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, true, {});
+    int64_t flags, bool deferred_check) {
+  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, deferred_check, true, {});
 }
 
 std::tuple<at::Tensor, at::Tensor> sparse_attn_fwd_lse_planned(
     const at::Tensor& q, const at::Tensor& kv, const at::Tensor& attn_sink,
     const at::Tensor& topk_idxs, double scale, const at::Tensor& plan,
-    const c10::optional<at::Tensor>& err, int64_t flags) {
-  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, true, plan);
+    const c10::optional<at::Tensor>& err, int64_t flags, bool deferred_check) {
+  return forward(q, kv, attn_sink, topk_idxs, scale, err, flags, deferred_check, true, plan);
 }
 
 // Merge n partials: o_parts bf16 [n, b, m, h, d], lse_parts fp32 [n, b, m, h].
@@ -290,26 +339,31 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> hc_split_sinkhorn_op(
 }  // namespace
 
 TORCH_LIBRARY(sa_amd, m) {
+  // deferred_check: with err = None, report bad indices into the device's
+  // mapped host flag (index_error_flag_address) instead of nowhere.
   m.def(
       "sparse_attn_fwd(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
-      "float scale, Tensor? err=None, int flags=0) -> Tensor");
+      "float scale, Tensor? err=None, int flags=0, bool deferred_check=False) -> Tensor");
   m.def(
       "sparse_attn_fwd_lse(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
-      "float scale, Tensor? err=None, int flags=0) -> (Tensor, Tensor)");
+      "float scale, Tensor? err=None, int flags=0, bool deferred_check=False) -> (Tensor, Tensor)");
   m.def("sparse_attn_merge(Tensor o_parts, Tensor lse_parts, Tensor? attn_sink=None) -> "
         "(Tensor, Tensor)");
   m.def(
-      "sparse_attn_plan(Tensor q, Tensor kv, Tensor topk_idxs, Tensor? err=None, int flags=0) "
-      "-> Tensor");
+      "sparse_attn_plan(Tensor q, Tensor kv, Tensor topk_idxs, Tensor? err=None, int flags=0, "
+      "bool deferred_check=False) -> Tensor");
   m.def(
       "sparse_attn_fwd_planned(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
-      "float scale, Tensor plan, Tensor? err=None, int flags=0) -> Tensor");
+      "float scale, Tensor plan, Tensor? err=None, int flags=0, bool deferred_check=False) "
+      "-> Tensor");
   m.def(
       "sparse_attn_fwd_lse_planned(Tensor q, Tensor kv, Tensor attn_sink, Tensor topk_idxs, "
-      "float scale, Tensor plan, Tensor? err=None, int flags=0) -> (Tensor, Tensor)");
+      "float scale, Tensor plan, Tensor? err=None, int flags=0, bool deferred_check=False) "
+      "-> (Tensor, Tensor)");
   m.def(
       "hc_split_sinkhorn(Tensor mixes, Tensor hc_scale, Tensor hc_base, int hc_mult=4, "
       "int sinkhorn_iters=20, float eps=1e-6, int flags=0) -> (Tensor, Tensor, Tensor)");
+  m.def("index_error_flag_address(int device) -> int");
 }
 
 TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
@@ -320,4 +374,9 @@ TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
   m.impl("sparse_attn_fwd_planned", &sparse_attn_fwd_planned);
   m.impl("sparse_attn_fwd_lse_planned", &sparse_attn_fwd_lse_planned);
   m.impl("hc_split_sinkhorn", &hc_split_sinkhorn_op);
+}
+
+// No tensor argument: registered for every dispatch key.
+TORCH_LIBRARY_IMPL(sa_amd, CatchAll, m) {
+  m.impl("index_error_flag_address", &index_error_flag_address);
 }

@@ -99,7 +99,6 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4_t;
-typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
 struct FwdParams {
@@ -234,6 +233,13 @@ __device__ __forceinline__ float sink_fold(float m, float l, float sink2, float&
   return a / den;
 }
 
+// Reports an index outside [-1, kv_len): *err = 1 as a system-scope store
+// (a vector store), so the word may also be mapped pinned host memory that
+// the host reads without synchronizing. Every writer stores the same value.
+__device__ __forceinline__ void flag_bad_index(int32_t* err) {
+  __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane j supplies the address
 // of 4 consecutive bf16 (row j/4, columns 4*(j%4)..+3 of a 4 x 16 block) and
 // receives column j of that block (4 values, one per row).
@@ -241,45 +247,38 @@ __device__ __forceinline__ bf16x4 lds_read_tr16(const uint8_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t*)((lds_u8_t*)(p)));
 }
 
-// LDS-DMA: every lane moves 16 (or 4) bytes from its own global address to
-// lds + lane * 16 (or 4); `lds` must be wave-uniform.
-__device__ __forceinline__ void lds_dma16(const void* gsrc, void* lds) {
-  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)((lds_u8_t*)(lds)), 16, 0, 0);
-}
-
-// The same 16-byte LDS-DMA issued from inline assembly, for pipelines that
-// read one LDS buffer while gathering into another: the compiler does not see
-// this as an LDS write, so it does not wait for the gather before every LDS
-// read. The caller must wait (vmcnt = 0, e.g. dma_barrier()) before any wave
-// reads the destination.
+// LDS-DMA issued from inline assembly: every lane moves 16 bytes from its own
+// global address to lds + lane * 16 (`lds` wave-uniform). Used by pipelines
+// that read one LDS buffer while gathering into another: the compiler does
+// not see this as an LDS write, so it does not wait for the gather before
+// every LDS read. The caller must wait (vmcnt = 0, e.g. dma_barrier()) before
+// any wave reads the destination. The LDS address goes in M0 through the
+// "{m0}" operand constraint, so the compiler writes M0 itself and knows what
+// it holds; s_nop 0 gives the wait state between that SALU write and the
+// load that reads M0.
 __device__ __forceinline__ void lds_dma16_async(const void* gsrc, void* lds) {
   const uint32_t lds_addr =
       __builtin_amdgcn_readfirstlane(uint32_t(reinterpret_cast<uintptr_t>((lds_u8_t*)(lds))));
   asm volatile(
-      "s_mov_b32 m0, %1\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, off"
       :
-      : "v"(gsrc), "s"(lds_addr)
-      : "memory", "m0");
+      : "v"(gsrc), "{m0}"(lds_addr)
+      : "memory");
 }
 
 // LDS-DMA of one 1 KiB row at a wave-uniform address: SGPR base `row` plus the
 // 32-bit lane offset 16 * lane, into LDS bytes lds_addr + 16 * lane. Measured
 // on gfx950, this form blocks the issuing wave for about 27 cycles against 46
 // for the same transfer with a 64-bit per-lane address.
+// M0 as in lds_dma16_async.
 __device__ __forceinline__ void lds_dma_row(const void* row, uint32_t lane_off, uint32_t lds_addr) {
   asm volatile(
-      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
       "global_load_lds_dwordx4 %0, %1"
       :
-      : "v"(lane_off), "s"(row), "s"(lds_addr)
-      : "memory", "m0");
-}
-
-__device__ __forceinline__ void lds_dma4(const void* gsrc, void* lds) {
-  __builtin_amdgcn_global_load_lds(gsrc, (lds_void_t*)((lds_u8_t*)(lds)), 4, 0, 0);
+      : "v"(lane_off), "s"(row), "{m0}"(lds_addr)
+      : "memory");
 }
 
 // Work-group barrier that orders LDS traffic only: waits for this wave's LDS
@@ -418,7 +417,7 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
       vals[i] = ok ? v : -1;
       c += ok ? 1 : 0;
     }
-    if (bad && p.err != nullptr) atomicOr(p.err, 1);
+    if (bad && p.err != nullptr) flag_bad_index(p.err);
     int incl = c;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
@@ -716,7 +715,7 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
       for (int u = 0; u < 4 * kIdxVec; ++u) count(v[u], qv[u]);
     }
   }
-  if (bad && p.err != nullptr) atomicOr(p.err, 1);
+  if (bad && p.err != nullptr) flag_bad_index(p.err);
   if (lane == 0 && nvalid != 0) atomicAdd(&s_nvalid, nvalid);
   __syncthreads();
 
@@ -958,20 +957,14 @@ constexpr int kTilePitch = kRowBytes + 48;
 // gather's.
 constexpr int kPPitch = 2 * kTileRows + 16;  // bytes per P column line
 constexpr int kTileCols = kTQ * kHeads;      // 128 score columns
-#ifndef SA_K_RING
-#define SA_K_RING 6
-#endif
-#ifndef SA_DMA_EVERY
-#define SA_DMA_EVERY 2
-#endif
 // K fragments of S^T = K . Q^T in flight: each ds_read_b128 is issued
 // kKRing - 1 MFMAs before the MFMA that consumes it.
-constexpr int kKRing = SA_K_RING;
+constexpr int kKRing = 6;
 // The 16 row gathers of a wave's share of the next step are issued one per
 // kDmaEvery MFMAs of S^T = K . Q^T. Every second MFMA of the first 32 (rows
 // 0..31, before the softmax work joins the slots) measured 1 % faster than
 // one per four spread over all 64.
-constexpr int kDmaEvery = SA_DMA_EVERY;
+constexpr int kDmaEvery = 2;
 static_assert(kDmaEvery * 16 <= 2 * (kDim / 16), "the gathers fit in the S^T MFMAs");
 
 struct TileSmem {

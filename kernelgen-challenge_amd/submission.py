@@ -11,21 +11,32 @@ There is no other code path: if the extension is not built, or the tensors are
 not on a GPU, the call raises.
 
 Index handling (see ``include/sparse_attn.h``): ``-1`` slots are excluded;
-any other index outside ``[0, kv_len)`` raises ``RuntimeError`` as the
-reference oracle does (``torch.gather`` at ``reference.py:28``). That check
-reads a device flag back, which synchronises the stream; turn it off with
-``set_index_check(False)`` or ``SPARSE_ATTN_CHECK=0`` for asynchronous calls
-(bad indices are then skipped silently and never read).
+any other index outside ``[0, kv_len)`` is never read and raises
+``RuntimeError``, as the reference oracle's ``torch.gather`` does
+(``reference.py:28``). The check has three modes (``set_index_check`` or the
+environment variable ``SPARSE_ATTN_CHECK``):
+
+* ``"deferred"`` (default): calls stay asynchronous. The kernels report a bad
+  index into a per-device flag in mapped pinned host memory; the next call on
+  that device (or :func:`check_index_errors`, which synchronizes) raises once
+  the flagged call has run. This is when a device-side error of the
+  reference's GPU ``torch.gather`` surfaces too: at a later point, not in
+  the call that launched it.
+* ``"sync"`` (``SPARSE_ATTN_CHECK=1``): every call waits for its kernels and
+  raises itself.
+* ``"off"`` (``SPARSE_ATTN_CHECK=0``): bad indices are skipped silently.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 import threading
 
 import torch
 
 __all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "sparse_attn_plan",
-           "IndexPlan", "set_index_check", "index_check_enabled", "set_path_flags",
+           "IndexPlan", "set_index_check", "index_check_enabled", "index_check_mode",
+           "check_index_errors", "set_path_flags",
            "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES",
            "hc_split_sinkhorn"]
 
@@ -33,8 +44,22 @@ _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 _EXT_PATH = os.path.join(_PKG_DIR, "lib", "sa_torch_ext.so")
 _lock = threading.Lock()
 _loaded = False
-_check = os.environ.get("SPARSE_ATTN_CHECK", "1") != "0"
+_CHECK_MODES = ("deferred", "sync", "off")
+
+
+def _mode_from(value) -> str:
+    if value is True or value in ("1", "sync"):
+        return "sync"
+    if value is False or value in ("0", "off"):
+        return "off"
+    if value in ("", "deferred"):
+        return "deferred"
+    raise ValueError(f"index check mode must be one of {_CHECK_MODES}, got {value!r}")
+
+
+_mode = _mode_from(os.environ.get("SPARSE_ATTN_CHECK", "deferred"))
 _flags = 0
+_err_flags = {}  # device index -> ctypes int32 over the mapped host flag
 
 # Kernel-path selection bits, as sa_args.flags in include/sparse_attn.h.
 FLAG_PER_QUERY = 1     # every query gathers its own rows
@@ -61,14 +86,54 @@ def load_extension() -> None:
         _loaded = True
 
 
-def set_index_check(enabled: bool) -> None:
-    """Turn the synchronous out-of-range index check on or off."""
-    global _check
-    _check = bool(enabled)
+def set_index_check(mode) -> None:
+    """Choose the out-of-range index check: ``"deferred"`` (default),
+    ``"sync"`` (``True``) or ``"off"`` (``False``)."""
+    global _mode
+    _mode = _mode_from(mode)
+
+
+def index_check_mode() -> str:
+    return _mode
 
 
 def index_check_enabled() -> bool:
-    return _check
+    return _mode != "off"
+
+
+def _err_flag(device):
+    """The device's deferred index-error flag (mapped pinned host memory)."""
+    i = device.index if device.index is not None else torch.cuda.current_device()
+    f = _err_flags.get(i)
+    if f is None:
+        with _lock:
+            f = _err_flags.get(i)
+            if f is None:
+                addr = torch.ops.sa_amd.index_error_flag_address(i)
+                f = _err_flags[i] = ctypes.c_int32.from_address(addr)
+    return f
+
+
+def _raise_pending(device):
+    """Deferred mode: raise if an earlier call on ``device`` met a bad index
+    (a plain host read; it does not wait for the GPU)."""
+    f = _err_flag(device)
+    if f.value != 0:
+        f.value = 0
+        raise RuntimeError("sparse_attn: an earlier call on this device had topk_idxs outside "
+                           "[-1, kv_len) (those slots were skipped)")
+
+
+def check_index_errors(device=None) -> None:
+    """Synchronize ``device`` (default: the current one) and raise
+    ``RuntimeError`` if a call on it since the last report met an index outside
+    ``[-1, kv_len)``. The explicit check point of the deferred mode."""
+    load_extension()
+    dev = torch.device("cuda") if device is None else torch.device(device)
+    if dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    torch.cuda.synchronize(dev)
+    _raise_pending(dev)
 
 
 def set_path_flags(flags: int) -> None:
@@ -87,6 +152,18 @@ def _checked_inputs(q, kv, attn_sink, topk_idxs):
     load_extension()
     # Same input handling as track-01/submission.py:995-998.
     return q.contiguous(), kv.contiguous(), attn_sink.contiguous(), topk_idxs.contiguous()
+
+
+def _check_args(device):
+    """(err tensor, deferred flag) of one call under the current mode: sync
+    mode gets a device word read back after the call, deferred mode first
+    reports an earlier call's bad index and then passes the host flag."""
+    if _mode == "sync":
+        return torch.zeros(1, dtype=torch.int32, device=device), False
+    if _mode == "deferred":
+        _raise_pending(device)
+        return None, True
+    return None, False
 
 
 def _raise_if_bad_index(err, kv_len):
@@ -146,8 +223,8 @@ def sparse_attn_plan(q, kv, topk_idxs):
     load_extension()
     idx_c = topk_idxs.contiguous()
     kv_c = kv.contiguous()
-    err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
-    ws = torch.ops.sa_amd.sparse_attn_plan(q.contiguous(), kv_c, idx_c, err, _flags)
+    err, deferred = _check_args(q.device)
+    ws = torch.ops.sa_amd.sparse_attn_plan(q.contiguous(), kv_c, idx_c, err, _flags, deferred)
     _raise_if_bad_index(err, kv.shape[1])
     return IndexPlan(ws, idx_c, topk_idxs, _plan_key(q, kv_c, topk_idxs))
 
@@ -167,13 +244,14 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, scale, plan=None):
         o:          [b, m, h, d]   bf16, a new tensor on q's device
     """
     q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
-    err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
+    err, deferred = _check_args(q.device)
     if plan is None:
-        o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags)
+        o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags,
+                                             deferred)
     else:
         plan._check(topk_idxs, _plan_key(q, kv_c, topk_idxs))
         o = torch.ops.sa_amd.sparse_attn_fwd_planned(q_c, kv_c, sink_c, plan.idx, float(scale),
-                                                     plan.workspace, err, _flags)
+                                                     plan.workspace, err, _flags, deferred)
     _raise_if_bad_index(err, kv.shape[1])
     return o
 
@@ -190,14 +268,14 @@ def sparse_attn_with_lse(q, kv, attn_sink, topk_idxs, scale, plan=None):
     ``plan`` as in :func:`sparse_attn`.
     """
     q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
-    err = torch.zeros(1, dtype=torch.int32, device=q.device) if _check else None
+    err, deferred = _check_args(q.device)
     if plan is None:
         o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse(q_c, kv_c, sink_c, idx_c, float(scale),
-                                                      err, _flags)
+                                                      err, _flags, deferred)
     else:
         plan._check(topk_idxs, _plan_key(q, kv_c, topk_idxs))
         o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse_planned(
-            q_c, kv_c, sink_c, plan.idx, float(scale), plan.workspace, err, _flags)
+            q_c, kv_c, sink_c, plan.idx, float(scale), plan.workspace, err, _flags, deferred)
     _raise_if_bad_index(err, kv.shape[1])
     return o, lse
 

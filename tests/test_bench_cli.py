@@ -19,7 +19,7 @@ REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, REPO)
 
 import bench  # noqa: E402
-import workloads as wl  # noqa: E402
+import sa_workloads as wl  # noqa: E402
 
 
 def run_bench(*args):

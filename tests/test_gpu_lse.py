@@ -12,7 +12,7 @@ import torch
 from oracle import sparse_attn_lse_fp64
 from test_gpu_parity import DEV, check, say
 import submission
-import workloads as wl
+import sa_workloads as wl
 
 pytestmark = pytest.mark.gpu
 

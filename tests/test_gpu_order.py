@@ -13,7 +13,7 @@ import pytest
 import torch
 
 import sa_capi
-import workloads as wl
+import sa_workloads as wl
 from test_gpu_parity import DEV, say
 from test_gpu_plan import case, windows
 

@@ -15,7 +15,7 @@ import torch
 
 from golden_io import fixture_names, load_fixture
 from oracle import sparse_attn_fp64, sparse_attn_ref
-import workloads as wl
+import sa_workloads as wl
 
 pytestmark = pytest.mark.gpu
 

@@ -9,7 +9,8 @@ import torch
 
 from test_gpu_parity import DEV, sampled_check, say
 import sa_capi
-import workloads as wl
+from sa_testutil import expect_plan
+import sa_workloads as wl
 
 pytestmark = pytest.mark.gpu
 
@@ -27,9 +28,9 @@ def case(b, m, kv_len, topk, seed, minus1=0.0):
     return q.to(DEV), kv.to(DEV), sink.to(DEV), idx.to(DEV), wl.SCALE
 
 
-def windows(b, m, kv_len, seed):
-    """Overlapping windows: shared tiles (with b * m at least the 256 CUs of
-    an MI355X, so that no query is split and the plan has tiles)."""
+def windows(b, m, kv_len, seed, tiles=True):
+    """Overlapping windows: shared tiles when b * m is large enough that no
+    query is split (asserted unless `tiles` is False)."""
     g = torch.Generator().manual_seed(seed)
     q = torch.randn(b, m, 16, 512, generator=g).to(torch.bfloat16)
     kv = torch.randn(b, kv_len, 512, generator=g).to(torch.bfloat16)
@@ -37,6 +38,8 @@ def windows(b, m, kv_len, seed):
     idx = torch.stack([torch.arange(256, dtype=torch.int32) + 3 * t for t in range(m)])
     idx = idx[None].repeat(b, 1, 1) % kv_len
     idx[:, ::5, 200:] = -1
+    if tiles:
+        expect_plan(q, kv, idx, 0, tiles=True, nsplit=1)
     return q.to(DEV), kv.to(DEV), sink.to(DEV), idx.to(DEV), wl.SCALE
 
 
@@ -77,7 +80,7 @@ def test_plan_serves_other_values(gpu_sa):
 
 
 def test_plan_refuses_changed_indices(gpu_sa):
-    q, kv, sink, idx, sc = windows(1, 16, 1000, seed=7)
+    q, kv, sink, idx, sc = windows(1, 16, 1000, seed=7, tiles=False)
     plan = gpu_sa.sparse_attn_plan(q, kv, idx)
     with pytest.raises(ValueError):
         gpu_sa.sparse_attn(q, kv, sink, idx.clone(), sc, plan=plan)      # other tensor
@@ -99,7 +102,8 @@ def test_plan_reports_bad_index(gpu_sa):
 def test_plan_of_an_aborting_tile(gpu_sa):
     """A tile whose scores jump far above its reference runs per query inside
     the shared-row kernel; planned, it does so again on every call."""
-    q, kv, sink, idx, sc = case(1, 256, 200, 128, seed=28)   # 256 queries: not split
+    q, kv, sink, idx, sc = case(1, 256, 200, 128, seed=28)
+    expect_plan(q, kv, idx, gpu_sa.FLAG_FORCE_TILES, tiles=True, nsplit=1)
     kv[0, 150] = (q[0, 2].float().mean(0) * 60).to(torch.bfloat16)
     idx[0, 2, :64] = torch.arange(64, dtype=torch.int32, device=DEV)
     idx[0, 2, 64] = 150

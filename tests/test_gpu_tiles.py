@@ -9,8 +9,9 @@ import pytest
 import torch
 
 from oracle import sparse_attn_fp64
+from sa_testutil import expect_plan
 from test_gpu_parity import DEV, check, config, sampled_check, say
-import workloads as wl
+import sa_workloads as wl
 
 pytestmark = pytest.mark.gpu
 
@@ -93,9 +94,9 @@ def test_tile_reference_jump_falls_back(gpu_sa):
     """A column whose scores jump far above its first step's max makes the tile
     hand itself to the per-query kernel (the tile kernel never rescales O):
     that tile's queries then match the per-query path bit for bit."""
-    # 256 queries (as many as CUs), so the plan does not split them and the
-    # tile path runs
+    # 256 queries: the plan must not split them, so the tile path runs
     q, kv, sink, idx, sc = rand_case(1, 256, 200, 128, seed=28)
+    expect_plan(q, kv, idx, FORCE_TILES, tiles=True, nsplit=1)
     kv[0, 150] = (q[0, 2].float().mean(0) * 60).to(torch.bfloat16)  # a row matching query 2
     idx[0, 2, :64] = torch.arange(64, dtype=torch.int32)   # first step: ordinary rows
     idx[0, 2, 64] = 150                                     # later: a huge score
@@ -166,6 +167,7 @@ def test_tile_sink_visible_and_exact_rows(gpu_sa):
 
 def test_tiles_deterministic(gpu_sa):
     q, kv, sink, idx, sc = rand_case(1, 260, 2000, 256, seed=27)
+    expect_plan(q, kv, idx, FORCE_TILES, tiles=True, nsplit=1)
     a = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
     b = run(q, kv, sink, idx, sc, flags=FORCE_TILES)
     assert torch.equal(a, b)
@@ -174,10 +176,11 @@ def test_tiles_deterministic(gpu_sa):
 def test_per_query_work_list_matches_direct_launch(gpu_sa):
     """A tile plan whose tiles all go to the per-query kernel (low overlap):
     the kernel strides over the work list the order kernel writes, one
-    work-group per CU, several queries per work-group (300 > 256 CUs), a
+    work-group per CU, several queries per work-group on 256 CUs, a
     ragged last tile. Each query must equal the direct per-query launch
     bit for bit, and the sampled oracle check must pass."""
     q, kv, sink, idx, sc = rand_case(1, 300, 16384, 256, seed=21, minus1=0.1)
+    expect_plan(q, kv, idx, 0, tiles=True, nsplit=1)
     o_l = run(q, kv, sink, idx, sc)
     o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY)
     # tiles 0..36 (8 random queries each: dense work ~8x the valid slots) run
@@ -194,10 +197,11 @@ def test_work_list_mixed_with_aborted_tile(gpu_sa):
     aborts at run time (scores jump far above its reference) in one call: the
     aborted tile's queries are appended to the work list by the tile kernel
     and computed by the per-query kernel launched next."""
-    # 256 queries (as many as CUs, so the plan does not split them); 512
-    # random rows of 8192 per query leave a tile's dense work ~7.6x its valid
-    # slots, so those tiles go to the per-query kernel
+    # 256 queries (the plan must not split them); 512 random rows of 8192 per
+    # query leave a tile's dense work ~7.6x its valid slots, so those tiles go
+    # to the per-query kernel
     q, kv, sink, idx, sc = rand_case(1, 256, 8192, 512, seed=22)
+    expect_plan(q, kv, idx, 0, tiles=True, nsplit=1)
     # queries 0..31: overlapping windows (shared tiles); 32..255 stay random
     # (per-query tiles from the index kernel)
     for t in range(32):

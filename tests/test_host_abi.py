@@ -251,6 +251,9 @@ def plan_full(host, a, cus):
     (1, 4, 100, 64, 2, True),            # half a tile
     (1, 3, 100, 64, 2, False),           # fewer queries than half a tile
     (1, 300, 100, 0, 0, False),          # no slots
+    (1, 256, 16384, 2 ** 27, 2, True),   # the largest topk the index kernel counts in 32 bits
+    (1, 256, 16384, 2 ** 27 + 1, 2, False),
+    (1, 256, 16384, 2 ** 31 - 1, 0, False),
 ])
 def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
     _, host = libs
@@ -307,6 +310,30 @@ def test_python_dropin_refuses_cpu_tensors():
         submission.sparse_attn(q, kv, sink, idx, 0.1)
     with pytest.raises(ValueError):
         submission.sparse_attn(q[0], kv, sink, idx, 0.1)
+
+
+def test_index_check_modes(monkeypatch):
+    """Default "deferred" (asynchronous); "sync" / "off" by name, by the
+    legacy booleans and by SPARSE_ATTN_CHECK=1 / 0; anything else refused."""
+    import importlib
+    import submission
+    try:
+        for env, mode in ((None, "deferred"), ("1", "sync"), ("0", "off"), ("sync", "sync"),
+                          ("deferred", "deferred")):
+            if env is None:
+                monkeypatch.delenv("SPARSE_ATTN_CHECK", raising=False)
+            else:
+                monkeypatch.setenv("SPARSE_ATTN_CHECK", env)
+            assert importlib.reload(submission).index_check_mode() == mode, env
+        for value, mode in ((True, "sync"), (False, "off"), ("deferred", "deferred")):
+            submission.set_index_check(value)
+            assert submission.index_check_mode() == mode
+            assert submission.index_check_enabled() == (mode != "off")
+        with pytest.raises(ValueError):
+            submission.set_index_check("sometimes")
+    finally:
+        monkeypatch.delenv("SPARSE_ATTN_CHECK", raising=False)
+        importlib.reload(submission)
 
 
 def test_torch_operator_registers(libs):
