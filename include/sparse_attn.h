@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 3
+#define SA_ABI_VERSION 4
 
 /* Return codes. */
 enum {
@@ -45,7 +45,9 @@ enum {
   SA_EINVAL = 1,        /* null pointer, negative size, bad stride or alignment */
   SA_EUNSUPPORTED = 2,  /* h != 16, d != 512, or a grid beyond the launch limit */
   SA_EWORKSPACE = 3,    /* workspace missing or smaller than sa_workspace_bytes */
-  SA_EHIP = 4           /* HIP runtime error (device query or launch) */
+  SA_EHIP = 4,          /* HIP runtime error (device query or launch) */
+  SA_ESCRATCH = 5       /* (ABI version 4) sa_forward_noalloc: the call needs more
+                           than SA_NOALLOC_SCRATCH_BYTES of workspace */
 };
 
 /* sa_args.flags bits (0 = let the library choose). */
@@ -176,6 +178,25 @@ int sa_merge(const sa_merge_args* a, void* hip_stream);
  * :313-322). Asynchronous; argument errors return before any device work.
  */
 int sa_plan_indices(const sa_args* a, void* hip_stream);
+
+/*
+ * Allocation-free forward (ABI version 4). No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments, results and launches as sa_forward, but the workspace is the
+ * library's own device array of SA_NOALLOC_SCRATCH_BYTES (one per GPU, held
+ * until the process ends); a->workspace and a->workspace_bytes are ignored.
+ * It calls no allocating routine. A call whose sa_workspace_bytes exceeds
+ * SA_NOALLOC_SCRATCH_BYTES returns SA_ESCRATCH before any device work (the
+ * five configurations of the contest's hot path need at most ~40 MiB);
+ * SA_FLAG_PLANNED is refused (SA_EINVAL): an index plan lives in a caller's
+ * workspace. Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race: serialize them.
+ * Nothing in the array has to start at zero, and each call overwrites what
+ * it reads before reading it.
+ */
+#define SA_NOALLOC_SCRATCH_BYTES (48u << 20)
+int sa_forward_noalloc(const sa_args* a, void* hip_stream);
 
 /* Kernels of one sa_forward call, in launch order. */
 enum {

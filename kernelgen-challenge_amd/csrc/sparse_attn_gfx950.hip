@@ -1473,6 +1473,31 @@ int current_cus(int* cus) {
   return SA_OK;
 }
 
+// Workspace of the allocation-free entry point (sa_forward_noalloc): one
+// array per GPU, created with the code object and held until the process
+// ends. Host code never passes `scratch` itself to a kernel (on the host the
+// name is only a stand-in for the symbol): it uses the device address that
+// hipGetSymbolAddress returns for the current device, looked up once per
+// device on that device's first sa_forward_noalloc call.
+constexpr size_t kScratchBytes = SA_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+uint8_t* g_scratch[kMaxDevices];  // device address of `scratch`, per device ordinal
+
+int current_scratch(uint8_t** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SA_EHIP;
+  uint8_t* p = __atomic_load_n(&g_scratch[dev], __ATOMIC_ACQUIRE);
+  if (p == nullptr) {
+    void* addr = nullptr;
+    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr)
+      return SA_EHIP;
+    p = static_cast<uint8_t*>(addr);
+    __atomic_store_n(&g_scratch[dev], p, __ATOMIC_RELEASE);  // a racing thread stores the same
+  }
+  *out = p;
+  return SA_OK;
+}
+
 // What forward() launches: every kernel of a call, or only the index plan.
 enum class Launch { kCall, kPlanOnly };
 int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
@@ -1491,6 +1516,9 @@ const char* sa_strerror(int code) {
     case SA_EUNSUPPORTED: return "unsupported shape (needs h == 16, d == 512)";
     case SA_EWORKSPACE: return "workspace missing or too small";
     case SA_EHIP: return "HIP runtime error";
+    case SA_ESCRATCH:
+      return "the call needs more workspace than sa_forward_noalloc holds "
+             "(SA_NOALLOC_SCRATCH_BYTES); use sa_forward with a workspace";
     default: return "unknown error";
   }
 }
@@ -1516,6 +1544,24 @@ int sa_forward_events(const sa_args* a, void* hip_stream, void* const* events,
                       uint32_t* launched) {
   if (launched != nullptr) *launched = 0u;
   return forward(a, static_cast<hipStream_t>(hip_stream), events, launched);
+}
+
+int sa_forward_noalloc(const sa_args* a, void* hip_stream) {
+  const int rc = sa::validate(a);
+  if (rc != SA_OK) return rc;
+  if ((a->flags & SA_FLAG_PLANNED) != 0) return SA_EINVAL;  // a plan lives in a caller's workspace
+  if (a->b == 0 || a->m == 0) return SA_OK;
+  int cus = 0;
+  const int qrc = current_cus(&cus);
+  if (qrc != SA_OK) return qrc;
+  if (sa::make_plan(a, cus).ws_bytes > kScratchBytes) return SA_ESCRATCH;
+  uint8_t* ws = nullptr;
+  const int src = current_scratch(&ws);
+  if (src != SA_OK) return src;
+  sa_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = kScratchBytes;
+  return forward(&b, static_cast<hipStream_t>(hip_stream), nullptr, nullptr);
 }
 
 int sa_plan_indices(const sa_args* a, void* hip_stream) {

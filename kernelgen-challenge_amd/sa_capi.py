@@ -16,7 +16,8 @@ import os
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libsparse_attn_gfx950.so")
 
-SA_OK, SA_EINVAL, SA_EUNSUPPORTED, SA_EWORKSPACE, SA_EHIP = range(5)
+SA_OK, SA_EINVAL, SA_EUNSUPPORTED, SA_EWORKSPACE, SA_EHIP, SA_ESCRATCH = range(6)
+SA_NOALLOC_SCRATCH_BYTES = 48 << 20
 SA_FLAG_PER_QUERY, SA_FLAG_FORCE_TILES, SA_FLAG_PLANNED = 1, 2, 4
 KERNELS = ("index", "order", "tile", "query", "combine")  # SA_KERNEL_* order
 SA_KERNEL_COUNT = len(KERNELS)
@@ -59,6 +60,7 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sa_abi_version.argtypes = []
     lib.sa_workspace_bytes.argtypes = [args_p, ctypes.POINTER(ctypes.c_size_t)]
     lib.sa_forward.argtypes = [args_p, ctypes.c_void_p]
+    lib.sa_forward_noalloc.argtypes = [args_p, ctypes.c_void_p]
     lib.sa_forward_events.argtypes = [args_p, ctypes.c_void_p,
                                       ctypes.POINTER(ctypes.c_void_p),
                                       ctypes.POINTER(ctypes.c_uint32)]
