@@ -35,7 +35,11 @@ line per scenario with the decode and prefill µs/call on each lane layout and
 the automatic choice, the frequency-weighted latency the reference's bench
 reports (``track-02/bench.py:50-53``), the HBM roofline of the prefill call
 (96 bytes read and 96 written per token) and the NumPy float32 restatement
-timed on the host as the CPU baseline. ``--copy-calibration`` runs a plain device copy of
+timed on the host as the CPU baseline. ``--moe`` times track 03's
+``fused_moe`` on the reference's eight workloads (``track-03/workloads.py:3-12``):
+one JSON line each with µs/call, algorithmic TFLOP/s, compulsory HBM bytes,
+every kernel's duration, the roofline of the longer GEMM kernel and the torch
+CPU restatement timed on a token sample. ``--copy-calibration`` runs a plain device copy of
 known size instead (for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters).
 """
 from __future__ import annotations
@@ -386,6 +390,146 @@ def bench_sinkhorn(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     return recs
 
 
+MOE_WORKLOADS = [  # track-03/workloads.py:3-12: label, M, K, N, E, topk
+    ("decode", 1, 2048, 1024, 8, 2), ("decode", 64, 2048, 1024, 8, 2),
+    ("decode", 1, 2048, 1024, 64, 6), ("decode", 64, 2048, 1024, 64, 6),
+    ("prefill", 512, 2048, 1024, 8, 2), ("prefill", 4096, 2048, 1024, 8, 2),
+    ("prefill", 512, 2048, 1024, 64, 6), ("prefill", 4096, 2048, 1024, 64, 6),
+]
+MOE_KERNEL_NAMES = {"route": "fm_route_kernel", "plan": "fm_plan_kernel",
+                    "gateup": "fm_gemm_kernel<true> / fm_skinny_kernel<true>",
+                    "down": "fm_gemm_kernel<false> / fm_skinny_kernel<false>",
+                    "reduce": "fm_reduce_kernel"}
+
+
+def moe_inputs(M, K, N, E, seed):
+    """track-03/test_correctness.py:15-21 on the GPU (seeded)."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    hidden = torch.randn(M, K, dtype=torch.bfloat16, generator=g, device="cuda")
+    w1 = torch.randn(E, 2 * N, K, dtype=torch.bfloat16, generator=g, device="cuda") * 0.02
+    w2 = torch.randn(E, K, N, dtype=torch.bfloat16, generator=g, device="cuda") * 0.02
+    score = torch.randn(M, E, dtype=torch.bfloat16, generator=g, device="cuda")
+    return hidden, w1, w2, score
+
+
+def moe_kernel_times(sets, topk, steps, warmup):
+    """Average launch duration (ms) of each fused_moe kernel (fm_forward_events)."""
+    import sa_capi
+    lib = sa_capi.fm_load()
+    stream = torch.cuda.current_stream()
+    outs = [torch.empty_like(s[0]) for s in sets]
+    args = [sa_capi.fm_make_args(*s, o, topk) for s, o in zip(sets, outs)]
+    wsz = max(sa_capi.fm_workspace_bytes(lib, a) for a in args)
+    ws = torch.empty(max(wsz, 1), dtype=torch.uint8, device="cuda")
+    for a in args:
+        a.workspace, a.workspace_bytes = ws.data_ptr(), wsz
+    nk = sa_capi.FM_KERNEL_COUNT
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2 * nk)] for _ in range(steps)]
+    for row in evs:
+        for e in row:
+            e.record(stream)
+    for i in range(warmup):
+        sa_capi.fm_check(lib, lib.fm_forward(ctypes.byref(args[i % len(args)]),
+                                             ctypes.c_void_p(stream.cuda_stream)))
+    torch.cuda.synchronize()
+    for i in range(steps):
+        sa_capi.fm_forward_events(lib, args[i % len(args)], stream.cuda_stream, evs[i])
+    torch.cuda.synchronize()
+    return {name: sum(evs[i][2 * k].elapsed_time(evs[i][2 * k + 1]) for i in range(steps)) / steps
+            for k, name in enumerate(sa_capi.FM_KERNELS)}
+
+
+def moe_cpu_baseline(hidden, w1, w2, score, topk, target_s=3.0, runs=3):
+    """The torch-CPU restatement (oracle/fused_moe_ref.py) on a bounded
+    sample of tokens, sized to about `target_s` seconds; median of `runs`."""
+    from oracle.fused_moe_ref import fused_moe_ref
+    M = hidden.shape[0]
+    perm = torch.randperm(M, generator=torch.Generator().manual_seed(7))
+
+    def run(n):
+        sel = perm[:n]
+        t0 = time.perf_counter()
+        fused_moe_ref(hidden[sel], w1, w2, score[sel], topk)
+        return time.perf_counter() - t0
+
+    run(min(M, 2))
+    n = min(M, 4)
+    dt = run(n)
+    while dt < target_s / 2 and n < M:
+        n = min(M, max(n + 1, int(n * target_s / max(dt, 1e-3))))
+        dt = run(n)
+    dt = statistics.median([dt] + [run(n) for _ in range(runs - 1)])
+    threads = torch.get_num_threads()
+    return {"value": round(dt / n * M * 1e6, 1), "unit": "us/call (extrapolated)",
+            "cores": threads, "kind": "port",
+            "sample": (f"{n} of {M} tokens (random, seed 7), median of {runs} runs of {dt:.3f} s; "
+                       f"torch-CPU restatement of track-03/reference/reference.py:10-35 "
+                       f"(oracle/fused_moe_ref.py, routed tokens only), {threads} threads")}
+
+
+def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
+    """One record per track-03 workload: µs/call of the drop-in
+    (submission.fused_moe), algorithmic TFLOP/s (6 N K flop per routed
+    (token, expert) pair: 4 N K gate-up, 2 N K down), compulsory HBM bytes
+    (the weights of the experts in use once, hidden, score and the output),
+    each kernel's average duration and the roofline of the longer GEMM."""
+    import submission
+    from oracle.fused_moe_ref import route
+    submission.load_extension()
+    recs = []
+    first = True
+    for label, M, K, N, E, topk in MOE_WORKLOADS:
+        sets = [moe_inputs(M, K, N, E, seed=100 + i) for i in range(nsets)]
+        fn = lambda h, a1, a2, sc, _s: submission.fused_moe(h, a1, a2, sc, topk)  # noqa: E731
+        tsets = [s for s in sets]
+        if first:
+            settle(fn, tsets, None, settle_s)
+            first = False
+        ms = time_calls(fn, tsets, None, steps, warmup)
+        times = moe_kernel_times(sets, topk, steps, warmup)
+        hidden, w1, w2, score = sets[0]
+        ids, _ = route(score.cpu(), topk)
+        used = int(torch.unique(ids).numel())
+        P = M * topk
+        flops = 6.0 * P * N * K
+        wbytes = used * 3.0 * N * K * 2
+        io = M * K * 2 * 2 + M * E * 2
+        t = ms * 1e-3
+        # the longer GEMM kernel and its share of the algorithmic work
+        dom = max(("gateup", "down"), key=times.get)
+        f_dom = (4.0 if dom == "gateup" else 2.0) * P * N * K
+        b_dom = used * (2.0 if dom == "gateup" else 1.0) * N * K * 2 + M * K * 2
+        td = times[dom] * 1e-3
+        if f_dom / (PEAK_MFMA_TFLOPS * 1e12) >= b_dom / (PEAK_HBM_GBPS * 1e9):
+            ach = f_dom / td / 1e12
+            roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_MFMA_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_TFLOPS, 4)}
+        else:
+            ach = b_dom / td / 1e9
+            roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
+                    "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4)}
+        roof.update({"traffic": None, "kernel": MOE_KERNEL_NAMES[dom],
+                     "kernel_us": round(times[dom] * 1e3, 2),
+                     "kernel_us_all": {MOE_KERNEL_NAMES[k]: round(v * 1e3, 2)
+                                       for k, v in times.items()}})
+        rec = {"metric": "fused_moe µs/call, TFLOP/s + HBM GB/s (% roofline)",
+               "value": round(flops / t / 1e12, 3), "unit": "TFLOP/s", "n_gpus": 1,
+               "steps": steps, "warmup": warmup, "us_per_call": round(ms * 1e3, 2),
+               "hbm_GBps_compulsory": round((wbytes + io) / t / 1e9, 1),
+               "higher_is_better": True, "dtype": "bf16",
+               "data": "synthetic (seeded device randn, weights x0.02, as the reference's test)",
+               "config": {"workload": f"fused_moe {label} M={M} K={K} N={N} E={E} topk={topk}",
+                          "pairs": P, "experts_used": used, "flops_alg": flops,
+                          "compulsory_bytes": wbytes + io, "input_sets_rotated": nsets},
+               "roofline": roof, "vs_baseline": None}
+        hc = [x.cpu() for x in sets[0]] if with_cpu else None
+        del sets, tsets, hidden, w1, w2, score
+        torch.cuda.empty_cache()
+        rec["cpu_baseline"] = moe_cpu_baseline(*hc, topk) if with_cpu else None
+        recs.append(rec)
+    return recs
+
+
 def copy_calibration(mib=1024, reps=5):
     """A plain device-to-device copy of `mib` MiB, `reps` times: under
     rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch scale the
@@ -414,6 +558,8 @@ def main():
                          "counter-collecting profiler, which serialises every dispatch)")
     ap.add_argument("--sinkhorn", action="store_true",
                     help="time track 02's hc_split_sinkhorn on its four scenarios instead")
+    ap.add_argument("--moe", action="store_true",
+                    help="time track 03's fused_moe on its eight workloads instead")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy of known size (PMC byte scaling)")
     args = ap.parse_args()
@@ -432,8 +578,14 @@ def main():
                                   args.settle):
             print(json.dumps(rec), flush=True)
         return
+    if args.moe:
+        for rec in bench_moe(args.steps, args.warmup, args.sets, not args.no_cpu, args.settle):
+            print(json.dumps(rec), flush=True)
+        return
     if args.all:
         for rec in bench_sinkhorn(args.steps, args.warmup, args.sets, False, args.settle):
+            print(json.dumps(rec), file=sys.stderr, flush=True)
+        for rec in bench_moe(args.steps, args.warmup, args.sets, False, args.settle):
             print(json.dumps(rec), file=sys.stderr, flush=True)
         for name in wl.CONFIGS:
             if name == args.config:

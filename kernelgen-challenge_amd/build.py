@@ -6,6 +6,8 @@ Outputs, all under ``kernelgen-challenge_amd/lib/``:
   built by ``hipcc --offload-arch=gfx950`` only.
 * ``libhc_sinkhorn_gfx950.so`` -- the track-02 ``hc_split_sinkhorn`` kernels +
   C-ABI (``include/hc_sinkhorn.h``), built the same way.
+* ``libfused_moe_gfx950.so`` -- the track-03 ``fused_moe`` kernels + C-ABI
+  (``include/fused_moe.h``), built the same way.
 * ``sa_torch_ext.so`` -- the PyTorch-ROCm operators ``torch.ops.sa_amd.*``
   (host C++ against torch's headers), linked to the two libraries above with
   an ``$ORIGIN`` rpath.
@@ -30,6 +32,7 @@ LIB_DIR = os.path.join(PKG_DIR, "lib")
 
 HIP_LIB = os.path.join(LIB_DIR, "libsparse_attn_gfx950.so")
 HC_LIB = os.path.join(LIB_DIR, "libhc_sinkhorn_gfx950.so")
+FM_LIB = os.path.join(LIB_DIR, "libfused_moe_gfx950.so")
 TORCH_EXT = os.path.join(LIB_DIR, "sa_torch_ext.so")
 HOST_TEST_LIB = os.path.join(LIB_DIR, "libsa_host_test.so")
 
@@ -73,7 +76,8 @@ def _atomic_target(path):
 
 def build_hip_lib(verbose=False):
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
-    for src, out in (("sparse_attn_gfx950.hip", HIP_LIB), ("hc_sinkhorn_gfx950.hip", HC_LIB)):
+    for src, out in (("sparse_attn_gfx950.hip", HIP_LIB), ("hc_sinkhorn_gfx950.hip", HC_LIB),
+                     ("fused_moe_gfx950.hip", FM_LIB)):
         tmp = _atomic_target(out)
         _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}",
               os.path.join(CSRC, src), "-o", tmp], verbose, strict=True)
@@ -96,7 +100,7 @@ def build_torch_ext(verbose=False):
     cmd += [f"-isystem{sysconfig.get_paths()['include']}"]
     cmd += [os.path.join(CSRC, "sa_torch.cpp"), "-o", tmp]
     cmd += [f"-L{p}" for p in libdirs] + [f"-L{LIB_DIR}", f"-L{ROCM}/lib"]
-    cmd += ["-lsparse_attn_gfx950", "-lhc_sinkhorn_gfx950", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+    cmd += ["-lsparse_attn_gfx950", "-lhc_sinkhorn_gfx950", "-lfused_moe_gfx950", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
             "-ltorch_hip", "-lamdhip64", "-Wl,-rpath,$ORIGIN"]
     cmd += [f"-Wl,-rpath,{p}" for p in libdirs]
     _run(cmd, verbose)
@@ -120,4 +124,4 @@ def build(verbose=False):
 
 if __name__ == "__main__":
     build(verbose="-q" not in sys.argv)
-    print(f"built {HIP_LIB}\n      {HC_LIB}\n      {TORCH_EXT}\n      {HOST_TEST_LIB}")
+    print(f"built {HIP_LIB}\n      {HC_LIB}\n      {FM_LIB}\n      {TORCH_EXT}\n      {HOST_TEST_LIB}")

@@ -1,0 +1,835 @@
+// fused_moe_gfx950.hip -- MI355X (gfx950, CDNA4) kernels and C-ABI of the
+// fused mixture-of-experts op of track 03 (include/fused_moe.h).
+//
+// Math (track-03/reference/reference.py:10-35), per token t: fp32 softmax of
+// the bf16 router scores, the topk largest (lower expert index first on
+// ties), optional renormalisation, bf16 weights; per selected expert e:
+// x = bf16(h . w1[e]^T), u = bf16(x[N:] * bf16(silu(x[:N]))),
+// y = bf16(u . w2[e]^T); out[t] = bf16 running sum over the selected experts
+// in ascending order of bf16(y * w_e). Every bf16 rounding sits where the
+// reference's bf16 tensors round, so the HIP path differs from the oracle
+// only by the order of the fp32 sums inside the two GEMMs.
+//
+// Kernels of one call
+// -------------------
+// fm_route_kernel   one wave per token: softmax over E, top-k by repeated
+//   wave-wide argmax on (weight, lower index), ids and bf16 weights written
+//   in ascending expert order (the order of the final sum).
+// fm_plan_kernel    one work-group: pairs (t, slot) counted per expert and
+//   listed by expert, tiles of up to `tile_rows` pairs of one expert.
+// fm_gemm_kernel<gated>   (tokens per expert > ~24) a tile of 128 pairs x
+//   256 weight rows per work-group, K in 64-wide stages through a 3-stage
+//   LDS ring filled by LDS-DMA (1 KiB per wave instruction, XOR-swizzled so
+//   the MFMA fragment reads are free of bank conflicts), 32x32x16 bf16 MFMA,
+//   fp32 accumulation. gated: w1 rows j (gate) and N + j (up) sit in the
+//   same lane and register, so silu(gate) * up is formed in the epilogue.
+//   Otherwise (w2): the epilogue multiplies by the pair's routing weight.
+// fm_skinny_kernel<gated, PB>  (few tokens per expert: decode) the weights
+//   are the streamed operand: each wave loads its 32 weight rows' MFMA
+//   fragments straight from HBM into registers (8 k-steps, 24-32 KiB, in
+//   flight per wave), the 16 * PB pairs' fragments likewise (L2-resident),
+//   and the 4 waves of a work-group split K and add their partial sums
+//   through LDS. 16x16x32 bf16 MFMA.
+// fm_reduce_kernel  out[t] = bf16 running sum of the token's topk weighted
+//   expert outputs, ascending expert order.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "fused_moe.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+constexpr int kMaxExperts = 256;
+constexpr int kMaxTopk = 32;
+
+// ---------------------------------------------------------------------------
+// workspace plan (host)
+// ---------------------------------------------------------------------------
+constexpr int kLargeRows = 128;   // pairs per tile of fm_gemm_kernel
+constexpr int kLargeCols = 256;   // weight rows per tile of fm_gemm_kernel
+constexpr int kBK = 64;           // k per LDS stage
+constexpr int kStages = 3;
+
+struct Plan {
+  int64_t P;            // pairs = M * topk
+  int tile_rows;        // pairs per tile
+  bool large;           // fm_gemm_kernel (else fm_skinny_kernel)
+  int pb;               // skinny: 16-pair blocks per tile (1 or 2)
+  int64_t max_tiles;    // upper bound on sum_e ceil(count_e / tile_rows)
+  size_t ids_off, wts_off, eoff_off, sorted_off, tiles_off, inter_off, y_off, bytes;
+};
+
+inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+Plan make_plan(const fm_args* a) {
+  Plan p{};
+  p.P = a->M * a->topk;
+  const double avg = double(p.P) / double(a->E);  // pairs per expert on average
+  if (a->flags & FM_FLAG_LARGE_TILES)
+    p.large = true;
+  else if (a->flags & FM_FLAG_SMALL_TILES)
+    p.large = false;
+  else
+    p.large = avg > 24.0;
+  p.pb = avg > 12.0 ? 2 : 1;
+  p.tile_rows = p.large ? kLargeRows : 16 * p.pb;
+  const int64_t nonempty = a->E < p.P ? a->E : p.P;
+  p.max_tiles = p.P / p.tile_rows + nonempty;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = round_up(off + bytes, 256);
+    return o;
+  };
+  p.ids_off = take(size_t(p.P) * 4);
+  p.wts_off = take(size_t(p.P) * 4);
+  p.eoff_off = take(size_t(a->E + 1) * 4);
+  p.sorted_off = take(size_t(p.P) * 4);
+  p.tiles_off = take(16 + size_t(p.max_tiles) * 16);  // count, then int4 per tile
+  p.inter_off = take(size_t(p.P) * size_t(a->N) * 2);
+  p.y_off = take(size_t(p.P) * size_t(a->K) * 2);
+  p.bytes = off;
+  return p;
+}
+
+int validate(const fm_args* a) {
+  if (a == nullptr) return FM_EINVAL;
+  if (a->M < 0 || a->K <= 0 || a->N <= 0 || a->E <= 0 || a->topk <= 0) return FM_EINVAL;
+  if (a->topk > a->E) return FM_EINVAL;
+  if (a->E > kMaxExperts || a->topk > kMaxTopk) return FM_EUNSUPPORTED;
+  if (a->K % kLargeCols != 0 || a->N % (kLargeCols / 2) != 0) return FM_EUNSUPPORTED;
+  if ((a->flags & ~uint32_t(FM_FLAG_LARGE_TILES | FM_FLAG_SMALL_TILES)) != 0 ||
+      (a->flags & FM_FLAG_LARGE_TILES && a->flags & FM_FLAG_SMALL_TILES))
+    return FM_EINVAL;
+  if (a->M == 0) return FM_OK;
+  if (!a->hidden || !a->w1 || !a->w2 || !a->score || !a->out) return FM_EINVAL;
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (!al16(a->hidden) || !al16(a->w1) || !al16(a->w2) || !al16(a->out)) return FM_EINVAL;
+  if ((reinterpret_cast<uintptr_t>(a->score) & 1u) != 0) return FM_EINVAL;
+  if (a->s_hidden < a->K || a->s_hidden % 8 != 0 || a->s_out < a->K || a->s_out % 8 != 0 ||
+      a->s_score < a->E)
+    return FM_EINVAL;
+  // 32-bit byte offsets: rows of hidden, of one expert's weights and of the
+  // intermediate buffers
+  const int64_t lim = int64_t(UINT32_MAX) - 4096;
+  if ((a->M - 1) * a->s_hidden * 2 + a->K * 2 > lim) return FM_EUNSUPPORTED;
+  if (2 * a->N * a->K * 2 > lim) return FM_EUNSUPPORTED;
+  if (a->M * a->topk * a->N * 2 > lim || a->M * a->topk * a->K * 2 > lim) return FM_EUNSUPPORTED;
+  return FM_OK;
+}
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16r(float x) {  // round to the nearest bf16
+  return static_cast<float>(static_cast<__bf16>(x));
+}
+
+// silu in fp32, as torch's bf16 silu computes it before its rounding
+__device__ __forceinline__ float silu(float x) { return x / (1.f + expf(-x)); }
+
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long y = __shfl_xor(x, o);
+    x = y > x ? y : x;
+  }
+  return x;
+}
+
+// LDS-DMA of 16 bytes per lane from SGPR base + 32-bit lane offset into
+// LDS bytes lds_addr + 16 * lane. The LDS address is handed to the compiler
+// as the M0 operand; s_nop 0 covers the wait state after its write. The
+// compiler does not see the LDS write: the caller waits (vmcnt) and
+// synchronizes before the data is read.
+__device__ __forceinline__ void lds_dma(const void* base, uint32_t lane_off, uint32_t lds_addr) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1"
+      :
+      : "v"(lane_off), "s"(base), "{m0}"(lds_addr)
+      : "memory");
+}
+
+// Work-group barrier that orders LDS traffic only (lgkmcnt = 0, then
+// s_barrier): LDS-DMA loads issued earlier keep flying across it, where
+// __syncthreads() would drain every outstanding global load.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt = max, expcnt = max, lgkmcnt = 0
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ============================================================================
+// routing
+// ============================================================================
+struct RouteParams {
+  const __bf16* score;
+  int64_t s_score;
+  int32_t* ids;     // [M, topk] ascending expert ids
+  float* wts;       // [M, topk] bf16-rounded weights (as fp32)
+  int64_t M;
+  int E, topk, renormalize;
+};
+
+// One wave per token; lane l holds experts l, l + 64, l + 128, l + 192.
+__global__ void __launch_bounds__(256) fm_route_kernel(const RouteParams p) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= p.M) return;
+  const __bf16* srow = p.score + t * p.s_score;
+  constexpr int kPer = kMaxExperts / 64;
+  float v[kPer];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < p.E ? static_cast<float>(srow[e]) : -INFINITY;
+    mx = fmaxf(mx, v[i]);
+  }
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    v[i] = (lane + 64 * i) < p.E ? expf(v[i] - mx) : 0.f;
+    sum += v[i];
+  }
+  sum = wave_sum(sum);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) v[i] = v[i] / sum;  // softmax weight (>= 0)
+  // top-k: repeated argmax over (weight, lower index); a weight's bits order
+  // like its value (weights are >= 0), the index goes in complemented
+  bool sel[kPer] = {};
+  float tot = 0.f;  // sum of the selected weights, in selection order
+  for (int r = 0; r < p.topk; ++r) {
+    unsigned long long key = 0ull;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int e = lane + 64 * i;
+      if (e < p.E && !sel[i]) {
+        const unsigned long long k = (static_cast<unsigned long long>(__float_as_uint(v[i])) << 32) |
+                                     (0xFFFFFFFFu - unsigned(e));
+        key = k > key ? k : key;
+      }
+    }
+    key = wave_max_u64(key);
+    const int win = int(0xFFFFFFFFu - unsigned(key & 0xFFFFFFFFull));
+    tot += __uint_as_float(unsigned(key >> 32));
+#pragma unroll
+    for (int i = 0; i < kPer; ++i)
+      if (lane + 64 * i == win) sel[i] = true;
+  }
+  // ascending-expert slot of each selected expert: ballots in expert order
+  int before = 0;
+  const unsigned long long below = (1ull << lane) - 1ull;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const unsigned long long m = __ballot(sel[i]);
+    if (sel[i]) {
+      const int slot = before + __popcll(m & below);
+      const float w = p.renormalize ? v[i] / tot : v[i];
+      p.ids[t * p.topk + slot] = lane + 64 * i;
+      p.wts[t * p.topk + slot] = bf16r(w);
+    }
+    before += __popcll(m);
+  }
+}
+
+// ============================================================================
+// plan: pairs by expert, tiles
+// ============================================================================
+struct PlanParams {
+  const int32_t* ids;
+  int32_t* eoff;      // [E + 1] first sorted position of each expert
+  int32_t* sorted;    // [P] pair ids (t * topk + slot) grouped by expert
+  int32_t* tiles;     // [0] = tile count, then int4 (expert, start, rows, 0) per tile
+  int64_t P;
+  int E, tile_rows;
+};
+
+__global__ void __launch_bounds__(1024) fm_plan_kernel(const PlanParams p) {
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_off[kMaxExperts + 1];
+  __shared__ int s_toff[kMaxExperts + 1];
+  __shared__ int s_cur[kMaxExperts];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < kMaxExperts; e += 1024) {
+    s_cnt[e] = 0;
+    s_cur[e] = 0;
+  }
+  __syncthreads();
+  for (int64_t i = tid; i < p.P; i += 1024) atomicAdd(&s_cnt[p.ids[i]], 1);
+  __syncthreads();
+  if (tid < 64) {  // exclusive scans of counts and tile counts over <= 256 experts
+    int carry = 0, tcarry = 0;
+    for (int c = 0; c < kMaxExperts / 64; ++c) {
+      const int e = 64 * c + tid;
+      const int v = e < p.E ? s_cnt[e] : 0;
+      const int tv = (v + p.tile_rows - 1) / p.tile_rows;
+      int incl = v, tincl = tv;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const int a = __shfl_up(incl, o);
+        const int b = __shfl_up(tincl, o);
+        if (tid >= o) {
+          incl += a;
+          tincl += b;
+        }
+      }
+      if (e < p.E) {
+        s_off[e] = carry + incl - v;
+        s_toff[e] = tcarry + tincl - tv;
+      }
+      carry += __shfl(incl, 63);
+      tcarry += __shfl(tincl, 63);
+    }
+    if (tid == 0) {
+      s_off[p.E] = carry;
+      s_toff[p.E] = tcarry;
+    }
+  }
+  __syncthreads();
+  for (int e = tid; e <= p.E; e += 1024) p.eoff[e] = s_off[e];
+  if (tid == 0) p.tiles[0] = s_toff[p.E];
+  for (int64_t i = tid; i < p.P; i += 1024) {
+    const int e = p.ids[i];
+    p.sorted[s_off[e] + atomicAdd(&s_cur[e], 1)] = int32_t(i);
+  }
+  for (int e = tid; e < p.E; e += 1024) {
+    const int n = s_cnt[e];
+    for (int k = 0; k * p.tile_rows < n; ++k) {
+      int32_t* tl = p.tiles + 4 + 4 * (s_toff[e] + k);
+      tl[0] = e;
+      tl[1] = s_off[e] + k * p.tile_rows;
+      tl[2] = min(p.tile_rows, n - k * p.tile_rows);
+      tl[3] = 0;
+    }
+  }
+}
+
+// ============================================================================
+// GEMMs
+// ============================================================================
+// GEMM 1 (gated): A row r of a tile = hidden[token of pair sorted[start + r]],
+//   weight rows = w1[e] rows j (gate) and N + j (up); output u to
+//   inter[start + r, j] (sorted pair order).
+// GEMM 2: A row r = inter[start + r], weight rows = w2[e] rows f (features);
+//   output bf16(bf16(y) * w_pair) to yw[pair, f] (pair = t * topk + slot).
+struct GemmParams {
+  const __bf16* a;       // hidden or inter
+  int64_t a_stride;      // elements per A row
+  const __bf16* w;       // w1 or w2
+  int64_t w_estride;     // elements per expert
+  const int32_t* sorted;
+  const int32_t* tiles;  // [0] = count, then int4 per tile
+  const float* wts;      // routing weights by pair (GEMM 2)
+  __bf16* out;           // inter [P, N] or yw [P, K]
+  int64_t out_stride;    // elements per output row
+  int kin;               // reduction length: K (GEMM 1) or N (GEMM 2)
+  int nout;              // GEMM 1: N (gate rows; up rows follow); GEMM 2: K
+  int topk;
+  int col_tiles;         // output-column tiles per pair tile
+};
+
+// ---- large tiles -------------------------------------------------------------
+// LDS stage: A 128 rows x 128 B, then B 256 rows x 128 B. Row r's 16-byte
+// chunk c (k = 8c..8c+7 of the stage) sits at chunk position c ^ ((r >> 1) & 7):
+// a 32x32x16 fragment read (lanes 0..15 = 16 consecutive rows, one chunk)
+// then covers all 64 banks once. An LDS-DMA instruction writes 8 rows
+// (1 KiB) lane-linearly, so each lane loads the global chunk that belongs at
+// its position.
+constexpr int kRowBytes = kBK * 2;                  // 128
+constexpr int kAStage = kLargeRows * kRowBytes;     // 16 KiB
+constexpr int kBStage = kLargeCols * kRowBytes;     // 32 KiB
+constexpr int kStage = kAStage + kBStage;           // 48 KiB
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+
+// The K loop and epilogue of one tile with NRB row blocks (of 32 pairs)
+// holding pairs: full tiles run NRB = 4, an expert's last tile fewer.
+template <bool kGated, int NRB>
+__device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* s_buf, const int* s_pair,
+                                          const float* s_wt, const uint8_t* abase,
+                                          const uint8_t* wbase, const uint32_t (&a_off)[4],
+                                          const uint32_t (&b_off)[8], uint32_t lds0, int start,
+                                          int rows, int ct) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+  const int nst = p.kin / kBK;
+  auto issue = [&](int st) {
+    const uint32_t sb = lds0 + uint32_t((st % kStages) * kStage);
+    const uint8_t* ab = abase + int64_t(st) * kRowBytes;
+    const uint8_t* bb = wbase + int64_t(st) * kRowBytes;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) lds_dma(ab, a_off[g], sb + uint32_t((4 * wave + g) * 1024));
+#pragma unroll
+    for (int g = 0; g < 8; ++g)
+      lds_dma(bb, b_off[g], sb + uint32_t(kAStage + (8 * wave + g) * 1024));
+  };
+
+  f32x16 acc[NRB][2];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[rb][cb][i] = 0.f;
+
+  issue(0);
+  if (nst > 1) issue(1);
+  for (int st = 0; st < nst; ++st) {
+    // this wave's loads of stage st are complete (12 loads per stage, the
+    // ones of stage st + 1 may still fly), then every wave's are
+    if (st + 1 < nst)
+      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    lds_barrier();
+    if (st + 2 < nst) issue(st + 2);  // into the buffer every wave finished reading
+    const uint8_t* sa = s_buf + (st % kStages) * kStage;
+    const uint8_t* sb = sa + kAStage;
+#pragma unroll
+    for (int kk = 0; kk < kBK / 16; ++kk) {
+      const int c = 2 * kk + hi;
+      bf16x8 bf[2];
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const int lr = 64 * wave + 32 * cb + l32;
+        bf[cb] = *reinterpret_cast<const bf16x8*>(sb + lr * kRowBytes + swz(lr, c) * 16);
+      }
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb) {
+        const int r = 32 * rb + l32;
+        const bf16x8 af = *reinterpret_cast<const bf16x8*>(sa + r * kRowBytes + swz(r, c) * 16);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[cb], acc[rb][cb], 0, 0, 0);
+      }
+    }
+  }
+
+  // epilogue: lane holds column l32 of each column block and pair rows
+  // 32 * rb + 8 * a + 4 * hi + b in register 4 * a + b
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int r = 32 * rb + 8 * a + 4 * hi + b;
+        if (r >= rows) continue;
+        const int ri = 4 * a + b;
+        if (kGated) {
+          const float g = bf16r(silu(bf16r(acc[rb][0][ri])));
+          const float u = bf16r(acc[rb][1][ri]) * g;
+          const int j = ct * (kLargeCols / 2) + 32 * wave + l32;
+          p.out[int64_t(start + r) * p.out_stride + j] = static_cast<__bf16>(u);
+        } else {
+          const int pair = s_pair[r];
+          const float w = s_wt[r];
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb) {
+            const int f = ct * kLargeCols + 64 * wave + 32 * cb + l32;
+            p.out[int64_t(pair) * p.out_stride + f] =
+                static_cast<__bf16>(bf16r(acc[rb][cb][ri]) * w);
+          }
+        }
+      }
+  }
+}
+
+template <bool kGated>
+__global__ void __launch_bounds__(256, 1) fm_gemm_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t s_buf[kStages * kStage];
+  __shared__ int s_pair[kLargeRows];
+  __shared__ float s_wt[kLargeRows];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const int tile = int(blockIdx.x) / p.col_tiles;
+  const int ct = int(blockIdx.x) % p.col_tiles;
+  if (tile >= p.tiles[0]) return;
+  const int32_t* tl = p.tiles + 4 + 4 * tile;
+  const int e = __builtin_amdgcn_readfirstlane(tl[0]);
+  const int start = __builtin_amdgcn_readfirstlane(tl[1]);
+  const int rows = __builtin_amdgcn_readfirstlane(tl[2]);
+
+  if (tid < kLargeRows) {
+    const int r = tid < rows ? tid : 0;
+    const int pair = p.sorted[start + r];
+    s_pair[tid] = pair;
+    if (!kGated) s_wt[tid] = p.wts[pair];
+  }
+  __syncthreads();
+
+  // Per-lane DMA sources. A: this wave's 4 instructions cover tile rows
+  // 32 * wave + 8 * g + lane / 8; B: its 8 instructions cover its own 64
+  // weight rows (LDS rows 64 * wave + 8 * g + lane / 8).
+  const int sub = lane >> 3;       // row within the instruction's 8
+  const int pos = lane & 7;        // chunk position within the row
+  uint32_t a_off[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int r = 32 * wave + 8 * g + sub;
+    const int c = swz(r, pos);  // the chunk whose swizzled position is `pos`
+    const int64_t arow = kGated ? int64_t(s_pair[r] / p.topk) : int64_t(start + (r < rows ? r : 0));
+    a_off[g] = uint32_t(arow * p.a_stride * 2 + c * 16);
+  }
+  uint32_t b_off[8];
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const int lr = 64 * wave + 8 * g + sub;   // LDS row of the B stage
+    const int cb = (lr >> 5) & 1;             // column block of the wave
+    const int i = lr & 31;
+    int wrow;
+    if (kGated)  // gate rows j, up rows N + j, j = ct * 128 + 32 * wave + i
+      wrow = (cb ? p.nout : 0) + ct * (kLargeCols / 2) + 32 * wave + i;
+    else         // features f = ct * 256 + lr
+      wrow = ct * kLargeCols + lr;
+    b_off[g] = uint32_t(int64_t(wrow) * p.kin * 2 + swz(lr, pos) * 16);
+  }
+  const uint8_t* abase = reinterpret_cast<const uint8_t*>(p.a);
+  const uint8_t* wbase = reinterpret_cast<const uint8_t*>(p.w + int64_t(e) * p.w_estride);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      uint32_t(reinterpret_cast<uintptr_t>((lds_u8_t*)s_buf)));
+
+  const int nrb = (rows + 31) / 32;  // 32-pair row blocks holding pairs
+#define FM_TILE(n) \
+  gemm_tile<kGated, n>(p, s_buf, s_pair, s_wt, abase, wbase, a_off, b_off, lds0, start, rows, ct)
+  switch (nrb) {
+    case 1: FM_TILE(1); break;
+    case 2: FM_TILE(2); break;
+    case 3: FM_TILE(3); break;
+    default: FM_TILE(4); break;
+  }
+#undef FM_TILE
+}
+
+// ---- skinny tiles (few pairs per expert) ------------------------------------------
+// Work-group: one tile of up to 16 * PB pairs x 16 output rows (gated: 16
+// gate rows j and the 16 up rows N + j; else 32 features in two blocks).
+// Wave w takes k-steps w, w + 4, ... (32 k each): 16x16x32 MFMA with the
+// weight rows as A (lane: row l % 16, k 8 * (l / 16)..+7 of the step) and the
+// pairs as B, both loaded straight into registers, 8 k-steps per batch.
+// D[weight row][pair]: lane holds pair l % 16, rows 4 * (l / 16) + i.
+constexpr int kSkBatch = 8;
+
+template <bool kGated, int PB>
+__global__ void __launch_bounds__(256) fm_skinny_kernel(const GemmParams p) {
+  __shared__ f32x4 s_red[4][2][PB][64];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  const int tile = int(blockIdx.x) / p.col_tiles;
+  const int ct = int(blockIdx.x) % p.col_tiles;
+  if (tile >= p.tiles[0]) return;
+  const int32_t* tl = p.tiles + 4 + 4 * tile;
+  const int e = tl[0];
+  const int start = tl[1];
+  const int rows = tl[2];
+
+  // weight rows of this lane's A fragments (block 0 and 1)
+  const __bf16* w = p.w + int64_t(e) * p.w_estride;
+  const __bf16* wr[2];
+  if (kGated) {
+    wr[0] = w + int64_t(16 * ct + li) * p.kin;              // gate j
+    wr[1] = w + int64_t(p.nout + 16 * ct + li) * p.kin;     // up j
+  } else {
+    wr[0] = w + int64_t(32 * ct + li) * p.kin;
+    wr[1] = w + int64_t(32 * ct + 16 + li) * p.kin;
+  }
+  // pair rows of this lane's B fragments
+  const __bf16* ar[PB];
+#pragma unroll
+  for (int q = 0; q < PB; ++q) {
+    const int r = 16 * q + li;
+    const int rr = r < rows ? r : 0;
+    const int64_t arow = kGated ? int64_t(p.sorted[start + rr] / p.topk) : int64_t(start + rr);
+    ar[q] = p.a + arow * p.a_stride;
+  }
+
+  f32x4 acc[2][PB];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int q = 0; q < PB; ++q) acc[b][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nsteps = p.kin / 32;
+  for (int s0 = wave; s0 < nsteps; s0 += 4 * kSkBatch) {
+    bf16x8 wf[kSkBatch][2];
+    bf16x8 af[kSkBatch][PB];
+#pragma unroll
+    for (int u = 0; u < kSkBatch; ++u) {
+      const int s = s0 + 4 * u;
+      if (s < nsteps) {
+        const int k = 32 * s + 8 * lg;
+#pragma unroll
+        for (int b = 0; b < 2; ++b) wf[u][b] = *reinterpret_cast<const bf16x8*>(wr[b] + k);
+#pragma unroll
+        for (int q = 0; q < PB; ++q) af[u][q] = *reinterpret_cast<const bf16x8*>(ar[q] + k);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSkBatch; ++u) {
+      if (s0 + 4 * u < nsteps) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int q = 0; q < PB; ++q)
+            acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[u][b], af[u][q], acc[b][q], 0,
+                                                                 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int q = 0; q < PB; ++q) s_red[wave][b][q][lane] = acc[b][q];
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      f32x4 s = s_red[0][b][q][lane];
+#pragma unroll
+      for (int v = 1; v < 4; ++v) s += s_red[v][b][q][lane];  // fixed order: deterministic
+      acc[b][q] = s;
+    }
+  // epilogue: pair r = 16 q + li, output rows 4 * lg + i
+#pragma unroll
+  for (int q = 0; q < PB; ++q) {
+    const int r = 16 * q + li;
+    if (r >= rows) continue;
+    if (kGated) {
+      bf16x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float g = bf16r(silu(bf16r(acc[0][q][i])));
+        o[i] = static_cast<__bf16>(bf16r(acc[1][q][i]) * g);
+      }
+      *reinterpret_cast<bf16x4*>(p.out + int64_t(start + r) * p.out_stride + 16 * ct + 4 * lg) = o;
+    } else {
+      const int pair = p.sorted[start + r];
+      const float wt = p.wts[pair];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        bf16x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = static_cast<__bf16>(bf16r(acc[b][q][i]) * wt);
+        *reinterpret_cast<bf16x4*>(p.out + int64_t(pair) * p.out_stride + 32 * ct + 16 * b +
+                                   4 * lg) = o;
+      }
+    }
+  }
+}
+
+// ============================================================================
+// final sum over each token's experts
+// ============================================================================
+struct ReduceParams {
+  const __bf16* yw;   // [M * topk, K]
+  __bf16* out;
+  int64_t s_out;
+  int64_t M;
+  int K, topk;
+};
+
+// One thread per 8 consecutive outputs of a token: the running bf16 sum over
+// slots 0..topk-1 (ascending experts), rounded after every add like the
+// reference's final_out += (reference.py:35).
+__global__ void __launch_bounds__(256) fm_reduce_kernel(const ReduceParams p) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  const int per = p.K / 8;
+  if (i >= p.M * per) return;
+  const int64_t t = i / per;
+  const int k = int(i % per) * 8;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const __bf16* y = p.yw + t * p.topk * int64_t(p.K) + k;
+  for (int j = 0; j < p.topk; ++j) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(y + int64_t(j) * p.K);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = bf16r(acc[c] + static_cast<float>(v[c]));
+  }
+  bf16x8 o;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) o[c] = static_cast<__bf16>(acc[c]);
+  *reinterpret_cast<bf16x8*>(p.out + t * p.s_out + k) = o;
+}
+
+int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t* launched) {
+  const int rc = validate(a);
+  if (rc != FM_OK) return rc;
+  if (a->M == 0) return FM_OK;
+  const Plan pl = make_plan(a);
+  if (a->workspace == nullptr || a->workspace_bytes < pl.bytes) return FM_EWORKSPACE;
+  auto mark = [&](int k, int after) -> bool {
+    if (after && launched != nullptr) *launched |= 1u << k;
+    if (events == nullptr) return true;
+    hipEvent_t ev = static_cast<hipEvent_t>(events[2 * k + after]);
+    return ev == nullptr || hipEventRecord(ev, stream) == hipSuccess;
+  };
+  auto launched_ok = [&](int k) { return hipGetLastError() == hipSuccess && mark(k, 1); };
+  uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+  int32_t* ids = reinterpret_cast<int32_t*>(ws + pl.ids_off);
+  float* wts = reinterpret_cast<float*>(ws + pl.wts_off);
+  int32_t* eoff = reinterpret_cast<int32_t*>(ws + pl.eoff_off);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + pl.sorted_off);
+  int32_t* tiles = reinterpret_cast<int32_t*>(ws + pl.tiles_off);
+  __bf16* inter = reinterpret_cast<__bf16*>(ws + pl.inter_off);
+  __bf16* yw = reinterpret_cast<__bf16*>(ws + pl.y_off);
+
+  RouteParams rp{};
+  rp.score = static_cast<const __bf16*>(a->score);
+  rp.s_score = a->s_score;
+  rp.ids = ids;
+  rp.wts = wts;
+  rp.M = a->M;
+  rp.E = int(a->E);
+  rp.topk = int(a->topk);
+  rp.renormalize = a->renormalize ? 1 : 0;
+  if (!mark(FM_KERNEL_ROUTE, 0)) return FM_EHIP;
+  hipLaunchKernelGGL(fm_route_kernel, dim3(unsigned((a->M + 3) / 4)), dim3(256), 0, stream, rp);
+  if (!launched_ok(FM_KERNEL_ROUTE)) return FM_EHIP;
+
+  PlanParams pp{};
+  pp.ids = ids;
+  pp.eoff = eoff;
+  pp.sorted = sorted;
+  pp.tiles = tiles;
+  pp.P = pl.P;
+  pp.E = int(a->E);
+  pp.tile_rows = pl.tile_rows;
+  if (!mark(FM_KERNEL_PLAN, 0)) return FM_EHIP;
+  hipLaunchKernelGGL(fm_plan_kernel, dim3(1), dim3(1024), 0, stream, pp);
+  if (!launched_ok(FM_KERNEL_PLAN)) return FM_EHIP;
+
+  GemmParams g1{};
+  g1.a = static_cast<const __bf16*>(a->hidden);
+  g1.a_stride = a->s_hidden;
+  g1.w = static_cast<const __bf16*>(a->w1);
+  g1.w_estride = 2 * a->N * a->K;
+  g1.sorted = sorted;
+  g1.tiles = tiles;
+  g1.wts = wts;
+  g1.out = inter;
+  g1.out_stride = a->N;
+  g1.kin = int(a->K);
+  g1.nout = int(a->N);
+  g1.topk = int(a->topk);
+  GemmParams g2 = g1;
+  g2.a = inter;
+  g2.a_stride = a->N;
+  g2.w = static_cast<const __bf16*>(a->w2);
+  g2.w_estride = a->K * a->N;
+  g2.out = yw;
+  g2.out_stride = a->K;
+  g2.kin = int(a->N);
+  g2.nout = int(a->K);
+  if (pl.large) {
+    g1.col_tiles = int(a->N / (kLargeCols / 2));
+    g2.col_tiles = int(a->K / kLargeCols);
+  } else {
+    g1.col_tiles = int(a->N / 16);
+    g2.col_tiles = int(a->K / 32);
+  }
+  const unsigned grid1 = unsigned(pl.max_tiles * g1.col_tiles);
+  const unsigned grid2 = unsigned(pl.max_tiles * g2.col_tiles);
+  if (!mark(FM_KERNEL_GATEUP, 0)) return FM_EHIP;
+  if (pl.large)
+    hipLaunchKernelGGL(fm_gemm_kernel<true>, dim3(grid1), dim3(256), 0, stream, g1);
+  else if (pl.pb == 1)
+    hipLaunchKernelGGL((fm_skinny_kernel<true, 1>), dim3(grid1), dim3(256), 0, stream, g1);
+  else
+    hipLaunchKernelGGL((fm_skinny_kernel<true, 2>), dim3(grid1), dim3(256), 0, stream, g1);
+  if (!launched_ok(FM_KERNEL_GATEUP)) return FM_EHIP;
+  if (!mark(FM_KERNEL_DOWN, 0)) return FM_EHIP;
+  if (pl.large)
+    hipLaunchKernelGGL(fm_gemm_kernel<false>, dim3(grid2), dim3(256), 0, stream, g2);
+  else if (pl.pb == 1)
+    hipLaunchKernelGGL((fm_skinny_kernel<false, 1>), dim3(grid2), dim3(256), 0, stream, g2);
+  else
+    hipLaunchKernelGGL((fm_skinny_kernel<false, 2>), dim3(grid2), dim3(256), 0, stream, g2);
+  if (!launched_ok(FM_KERNEL_DOWN)) return FM_EHIP;
+
+  ReduceParams rd{};
+  rd.yw = yw;
+  rd.out = static_cast<__bf16*>(a->out);
+  rd.s_out = a->s_out;
+  rd.M = a->M;
+  rd.K = int(a->K);
+  rd.topk = int(a->topk);
+  const int64_t threads = a->M * (a->K / 8);
+  if (!mark(FM_KERNEL_REDUCE, 0)) return FM_EHIP;
+  hipLaunchKernelGGL(fm_reduce_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0,
+                     stream, rd);
+  if (!launched_ok(FM_KERNEL_REDUCE)) return FM_EHIP;
+  return FM_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fm_abi_version(void) { return FM_ABI_VERSION; }
+
+const char* fm_strerror(int code) {
+  switch (code) {
+    case FM_OK: return "ok";
+    case FM_EINVAL: return "invalid argument (null pointer, size, stride, alignment or flags)";
+    case FM_EUNSUPPORTED:
+      return "unsupported shape (needs K % 256 == 0, N % 128 == 0, E <= 256, topk <= 32 and "
+             "sizes within 32-bit offsets)";
+    case FM_EWORKSPACE: return "workspace missing or too small";
+    case FM_EHIP: return "HIP runtime error";
+    default: return "unknown error";
+  }
+}
+
+int fm_workspace_bytes(const fm_args* a, size_t* out_bytes) {
+  if (out_bytes == nullptr) return FM_EINVAL;
+  const int rc = validate(a);
+  if (rc != FM_OK) return rc;
+  *out_bytes = a->M == 0 ? 0 : make_plan(a).bytes;
+  return FM_OK;
+}
+
+int fm_forward(const fm_args* a, void* hip_stream) {
+  return forward(a, static_cast<hipStream_t>(hip_stream), nullptr, nullptr);
+}
+
+int fm_forward_events(const fm_args* a, void* hip_stream, void* const* events,
+                      uint32_t* launched) {
+  if (launched != nullptr) *launched = 0u;
+  return forward(a, static_cast<hipStream_t>(hip_stream), events, launched);
+}
+
+}  // extern "C"

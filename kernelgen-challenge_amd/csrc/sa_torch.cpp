@@ -1,10 +1,11 @@
-// sa_torch.cpp -- thin PyTorch-ROCm operator over the sparse_attn C-ABI.
+// sa_torch.cpp -- thin PyTorch-ROCm operators over the C-ABIs of this package.
 //
 // Registers torch.ops.sa_amd.sparse_attn_fwd (o), sparse_attn_fwd_lse
 // (o, lse), sparse_attn_merge (o, lse of merged partials), sparse_attn_plan
 // (the index plan of a topk_idxs tensor) and the planned forwards
-// sparse_attn_fwd_planned / sparse_attn_fwd_lse_planned, and the track-02
-// operator hc_split_sinkhorn (pre, post, comb) over include/hc_sinkhorn.h.
+// sparse_attn_fwd_planned / sparse_attn_fwd_lse_planned, the track-02
+// operator hc_split_sinkhorn (pre, post, comb) over include/hc_sinkhorn.h and
+// the track-03 operator fused_moe over include/fused_moe.h.
 // They check devices and dtypes, allocate the outputs (like
 // track-01/submission.py:1000 and track-02/submission.py:353-355) and the
 // workspace through the caching allocator, and call the C-ABIs on the
@@ -17,6 +18,7 @@
 
 #include <mutex>
 
+#include "fused_moe.h"
 #include "hc_sinkhorn.h"
 #include "sparse_attn.h"
 
@@ -336,6 +338,62 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> hc_split_sinkhorn_op(
   return {pre, post, comb};
 }
 
+// track-03: hidden bf16 [M, K], w1 bf16 [E, 2N, K], w2 bf16 [E, K, N],
+// score bf16 [M, E]. Returns out bf16 [M, K] (track-03/submission.py:293-294
+// allocates it the same way).
+at::Tensor fused_moe_op(const at::Tensor& hidden, const at::Tensor& w1, const at::Tensor& w2,
+                        const at::Tensor& score, int64_t topk, bool renormalize,
+                        int64_t flags) {
+  TORCH_CHECK_VALUE(hidden.dim() == 2 && w1.dim() == 3 && w2.dim() == 3 && score.dim() == 2,
+                    "expected hidden [M, K], w1 [E, 2N, K], w2 [E, K, N], score [M, E]");
+  for (const at::Tensor* t : {&hidden, &w1, &w2, &score})
+    TORCH_CHECK_TYPE(t->scalar_type() == at::kBFloat16,
+                     "fused_moe: hidden, w1, w2 and score must be bfloat16");
+  TORCH_CHECK(hidden.is_cuda() && w1.device() == hidden.device() &&
+                  w2.device() == hidden.device() && score.device() == hidden.device(),
+              "fused_moe: all inputs must be on the same GPU");
+  const int64_t M = hidden.size(0), K = hidden.size(1), E = w1.size(0), N = w2.size(2);
+  TORCH_CHECK_VALUE(w1.size(1) == 2 * N && w1.size(2) == K && w2.size(0) == E &&
+                        w2.size(1) == K && score.size(0) == M && score.size(1) == E,
+                    "fused_moe: shapes hidden ", hidden.sizes(), ", w1 ", w1.sizes(), ", w2 ",
+                    w2.sizes(), ", score ", score.sizes(), " do not match");
+  TORCH_CHECK_VALUE(flags >= 0 && flags <= 0xFFFFFFFFll, "bad flags ", flags);
+  const c10::DeviceGuard guard(hidden.device());
+  const at::Tensor h = hidden.contiguous(), a1 = w1.contiguous(), a2 = w2.contiguous(),
+                   sc = score.contiguous();
+  at::Tensor out = at::empty({M, K}, hidden.options());
+  fm_args a{};
+  a.hidden = h.data_ptr();
+  a.w1 = a1.data_ptr();
+  a.w2 = a2.data_ptr();
+  a.score = sc.data_ptr();
+  a.out = out.data_ptr();
+  a.M = M;
+  a.K = K;
+  a.N = N;
+  a.E = E;
+  a.topk = topk;
+  a.s_hidden = K;
+  a.s_score = E;
+  a.s_out = K;
+  a.renormalize = renormalize ? 1 : 0;
+  a.flags = static_cast<uint32_t>(flags);
+  size_t ws = 0;
+  auto rc_check = [](int rc) {
+    TORCH_CHECK_VALUE(rc != FM_EINVAL && rc != FM_EUNSUPPORTED, "fused_moe: ", fm_strerror(rc));
+    TORCH_CHECK(rc == FM_OK, "fused_moe: ", fm_strerror(rc));
+  };
+  rc_check(fm_workspace_bytes(&a, &ws));
+  at::Tensor workspace;
+  if (ws > 0) {
+    workspace = at::empty({static_cast<int64_t>(ws)}, hidden.options().dtype(at::kByte));
+    a.workspace = workspace.data_ptr();
+    a.workspace_bytes = ws;
+  }
+  rc_check(fm_forward(&a, c10::hip::getCurrentHIPStream().stream()));
+  return out;
+}
+
 }  // namespace
 
 TORCH_LIBRARY(sa_amd, m) {
@@ -364,6 +422,9 @@ TORCH_LIBRARY(sa_amd, m) {
       "hc_split_sinkhorn(Tensor mixes, Tensor hc_scale, Tensor hc_base, int hc_mult=4, "
       "int sinkhorn_iters=20, float eps=1e-6, int flags=0) -> (Tensor, Tensor, Tensor)");
   m.def("index_error_flag_address(int device) -> int");
+  m.def(
+      "fused_moe(Tensor hidden, Tensor w1, Tensor w2, Tensor score, int topk, "
+      "bool renormalize=False, int flags=0) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
@@ -374,6 +435,7 @@ TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
   m.impl("sparse_attn_fwd_planned", &sparse_attn_fwd_planned);
   m.impl("sparse_attn_fwd_lse_planned", &sparse_attn_fwd_lse_planned);
   m.impl("hc_split_sinkhorn", &hc_split_sinkhorn_op);
+  m.impl("fused_moe", &fused_moe_op);
 }
 
 // No tensor argument: registered for every dispatch key.

@@ -160,3 +160,80 @@ def hc_make_args(mixes, scale, base, pre, post, comb, iters=20, eps=1e-6, flags=
     a.n = mixes.numel() // 24
     a.hc_mult, a.iters, a.eps, a.flags = hc_mult, iters, eps, flags
     return a
+
+
+# ---------------------------------------------------------------------------
+# track-03 fused_moe (include/fused_moe.h)
+# ---------------------------------------------------------------------------
+FM_LIB_PATH = os.path.join(_HERE, "lib", "libfused_moe_gfx950.so")
+FM_OK, FM_EINVAL, FM_EUNSUPPORTED, FM_EWORKSPACE, FM_EHIP = range(5)
+FM_FLAG_LARGE_TILES, FM_FLAG_SMALL_TILES = 1, 2
+FM_KERNELS = ("route", "plan", "gateup", "down", "reduce")  # FM_KERNEL_* order
+FM_KERNEL_COUNT = len(FM_KERNELS)
+
+
+class FmArgs(ctypes.Structure):
+    """``struct fm_args`` (include/fused_moe.h)."""
+    _fields_ = [
+        ("hidden", ctypes.c_void_p), ("w1", ctypes.c_void_p), ("w2", ctypes.c_void_p),
+        ("score", ctypes.c_void_p), ("out", ctypes.c_void_p),
+        ("M", ctypes.c_int64), ("K", ctypes.c_int64), ("N", ctypes.c_int64),
+        ("E", ctypes.c_int64), ("topk", ctypes.c_int64),
+        ("s_hidden", ctypes.c_int64), ("s_score", ctypes.c_int64), ("s_out", ctypes.c_int64),
+        ("renormalize", ctypes.c_int32), ("flags", ctypes.c_uint32),
+        ("workspace", ctypes.c_void_p), ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+def fm_load(path: str = FM_LIB_PATH) -> ctypes.CDLL:
+    """Load the track-03 library and declare its entry points."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    args_p = ctypes.POINTER(FmArgs)
+    lib.fm_abi_version.restype = ctypes.c_int
+    lib.fm_abi_version.argtypes = []
+    lib.fm_strerror.restype = ctypes.c_char_p
+    lib.fm_strerror.argtypes = [ctypes.c_int]
+    lib.fm_workspace_bytes.argtypes = [args_p, ctypes.POINTER(ctypes.c_size_t)]
+    lib.fm_forward.argtypes = [args_p, ctypes.c_void_p]
+    lib.fm_forward_events.argtypes = [args_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p),
+                                      ctypes.POINTER(ctypes.c_uint32)]
+    return lib
+
+
+def fm_make_args(hidden, w1, w2, score, out, topk, renormalize=False, flags=0) -> FmArgs:
+    """fm_args for torch tensors hidden [M, K], w1 [E, 2N, K], w2 [E, K, N],
+    score [M, E], out [M, K] (rows with unit inner stride)."""
+    a = FmArgs()
+    a.hidden, a.w1, a.w2 = hidden.data_ptr(), w1.data_ptr(), w2.data_ptr()
+    a.score, a.out = score.data_ptr(), out.data_ptr()
+    a.M, a.K = hidden.shape
+    a.E, a.N = w1.shape[0], w2.shape[2]
+    a.topk = topk
+    a.s_hidden, a.s_score, a.s_out = hidden.stride(0), score.stride(0), out.stride(0)
+    a.renormalize = 1 if renormalize else 0
+    a.flags = flags
+    return a
+
+
+def fm_check(lib, rc: int, what: str = "fused_moe") -> None:
+    if rc != FM_OK:
+        raise RuntimeError(f"{what}: {lib.fm_strerror(rc).decode()} (code {rc})")
+
+
+def fm_workspace_bytes(lib, a: FmArgs) -> int:
+    n = ctypes.c_size_t(0)
+    fm_check(lib, lib.fm_workspace_bytes(ctypes.byref(a), ctypes.byref(n)), "fm_workspace_bytes")
+    return n.value
+
+
+def fm_forward_events(lib, a: FmArgs, stream: int, events) -> int:
+    """fm_forward_events with 2 * FM_KERNEL_COUNT torch.cuda.Event objects (or
+    None entries); returns the bit mask of launched kernels."""
+    handles = (ctypes.c_void_p * (2 * FM_KERNEL_COUNT))(
+        *[(ev.cuda_event if ev is not None else None) for ev in events])
+    launched = ctypes.c_uint32(0)
+    fm_check(lib, lib.fm_forward_events(ctypes.byref(a), ctypes.c_void_p(stream), handles,
+                                        ctypes.byref(launched)), "fm_forward_events")
+    return launched.value

@@ -38,7 +38,7 @@ __all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "sparse_a
            "IndexPlan", "set_index_check", "index_check_enabled", "index_check_mode",
            "check_index_errors", "set_path_flags",
            "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES",
-           "hc_split_sinkhorn"]
+           "hc_split_sinkhorn", "fused_moe"]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 _EXT_PATH = os.path.join(_PKG_DIR, "lib", "sa_torch_ext.so")
@@ -307,6 +307,9 @@ def sparse_attn_merge(o_parts, lse_parts, attn_sink=None):
     return torch.ops.sa_amd.sparse_attn_merge(o_parts, lse_parts, attn_sink)
 
 
-# Track 02's entry point, so that ``from submission import hc_split_sinkhorn``
-# (track-02/test_correctness.py:14, bench.py:14) finds it here as well.
+# Track 02's and track 03's entry points, so that ``from submission import
+# hc_split_sinkhorn`` (track-02/test_correctness.py:14, bench.py:14) and
+# ``from submission import fused_moe`` (track-03/test_correctness.py:9) find
+# them here as well.
 from hc_sinkhorn import hc_split_sinkhorn  # noqa: E402
+from moe import fused_moe  # noqa: E402

@@ -29,7 +29,9 @@ REFERENCE = "/root/reference"
 HARNESS_IMPORTS = {"submission", "reference", "workloads", "torch", "triton", "pytest",
                    "sys", "math", "argparse"}
 HARNESS_SCRIPTS = ["track-01/test_correctness.py", "track-01/bench.py", "track-01/profile.py",
-                   "track-02/test_correctness.py", "track-02/bench.py", "track-02/profile.py"]
+                   "track-02/test_correctness.py", "track-02/bench.py", "track-02/profile.py",
+                   "track-03/test_correctness.py", "track-03/test_reference.py",
+                   "track-03/test_workloads.py"]
 
 
 def package_modules():
@@ -51,7 +53,7 @@ def test_package_shadows_nothing_but_submission():
 
 def test_submission_exports_every_track_entry_point():
     import submission
-    for name in ("sparse_attn", "hc_split_sinkhorn"):
+    for name in ("sparse_attn", "hc_split_sinkhorn", "fused_moe"):
         assert callable(getattr(submission, name, None)), name
 
 
