@@ -35,7 +35,9 @@ line per scenario with the decode and prefill µs/call on each lane layout and
 the automatic choice, the frequency-weighted latency the reference's bench
 reports (``track-02/bench.py:50-53``), the HBM roofline of the prefill call
 (96 bytes read and 96 written per token) and the NumPy float32 restatement
-timed on the host as the CPU baseline. ``--moe`` times track 03's
+timed on the host as the CPU baseline. ``--contest`` times the ten contest shapes of the reference's harness
+(``track-01/workloads.py:15-26``), one JSON line each, with the torch-CPU
+restatement timed beside them. ``--moe`` times track 03's
 ``fused_moe`` on the reference's eight workloads (``track-03/workloads.py:3-12``):
 one JSON line each with µs/call, algorithmic TFLOP/s, compulsory HBM bytes,
 every kernel's duration, the roofline of the longer GEMM kernel and the torch
@@ -530,6 +532,50 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     return recs
 
 
+def bench_contest(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
+    """One record per contest shape of the reference's harness
+    (track-01/workloads.py:15-26, inputs as its make_inputs :29-37, seeded):
+    µs/call of the drop-in, algorithmic TFLOP/s, and the torch-CPU
+    restatement timed on a query sample beside it. The reference publishes
+    only speedups over its own torch oracle on these shapes
+    (track-01/bench.py:26-47), so the CPU time is the comparable figure here."""
+    import submission
+    submission.load_extension()
+    submission.set_index_check("deferred")
+    recs = []
+    first = True
+    for label, kind, b, m, kv_len, topk in wl.CONTEST_WORKLOADS:
+        sets = []
+        for i in range(nsets):
+            g = torch.Generator(device="cuda").manual_seed(i)
+            q = torch.randn(b, m, H, D, dtype=torch.bfloat16, device="cuda", generator=g)
+            kv = torch.randn(b, kv_len, D, dtype=torch.bfloat16, device="cuda", generator=g)
+            sink = torch.randn(H, dtype=torch.float32, device="cuda", generator=g)
+            idx = torch.randint(0, kv_len, (b, m, topk), dtype=torch.int32, device="cuda",
+                                generator=g)
+            sets.append((q, kv, sink, idx))
+        if first:
+            settle(submission.sparse_attn, sets, wl.SCALE, settle_s)
+            first = False
+        ms = time_calls(submission.sparse_attn, sets, wl.SCALE, steps, warmup)
+        n_valid = b * m * topk
+        flops = 4.0 * H * D * n_valid
+        rec = {"op": "sparse_attn", "workload": label, "kind": kind,
+               "shape": {"b": b, "m": m, "kv_len": kv_len, "topk": topk},
+               "us_per_call": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
+               "gathered_kv_GBps": round(n_valid * D * 2 / (ms * 1e-3) / 1e9, 1),
+               "dtype": "bf16", "data": "synthetic (seeded device randn, as make_inputs)"}
+        if with_cpu:
+            q, kv, sink, idx = (t.cpu() for t in sets[0])
+            cb = cpu_baseline((q, kv, sink, idx, wl.SCALE), target_s=1.5)
+            rec["cpu_baseline"] = cb
+            rec["speedup_vs_cpu"] = round(cb["us_per_call_extrapolated"] / rec["us_per_call"], 1)
+        recs.append(rec)
+        del sets
+        torch.cuda.empty_cache()
+    return recs
+
+
 def copy_calibration(mib=1024, reps=5):
     """A plain device-to-device copy of `mib` MiB, `reps` times: under
     rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch scale the
@@ -558,6 +604,8 @@ def main():
                          "counter-collecting profiler, which serialises every dispatch)")
     ap.add_argument("--sinkhorn", action="store_true",
                     help="time track 02's hc_split_sinkhorn on its four scenarios instead")
+    ap.add_argument("--contest", action="store_true",
+                    help="time the reference harness's ten contest shapes instead")
     ap.add_argument("--moe", action="store_true",
                     help="time track 03's fused_moe on its eight workloads instead")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -576,6 +624,11 @@ def main():
     if args.sinkhorn:
         for rec in bench_sinkhorn(args.steps, args.warmup, args.sets, not args.no_cpu,
                                   args.settle):
+            print(json.dumps(rec), flush=True)
+        return
+    if args.contest:
+        for rec in bench_contest(args.steps, args.warmup, args.sets, not args.no_cpu,
+                                 args.settle):
             print(json.dumps(rec), flush=True)
         return
     if args.moe:

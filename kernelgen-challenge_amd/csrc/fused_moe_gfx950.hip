@@ -61,7 +61,7 @@ struct Plan {
   int64_t P;            // pairs = M * topk
   int tile_rows;        // pairs per tile
   bool large;           // fm_gemm_kernel (else fm_skinny_kernel)
-  int pb;               // skinny: 16-pair blocks per tile (1 or 2)
+  int pb;               // small tiles: 16-pair blocks per tile (1, 2 or 4)
   int64_t max_tiles;    // upper bound on sum_e ceil(count_e / tile_rows)
   size_t ids_off, wts_off, eoff_off, sorted_off, tiles_off, inter_off, y_off, bytes;
 };
@@ -78,7 +78,9 @@ Plan make_plan(const fm_args* a) {
     p.large = false;
   else
     p.large = avg > 24.0;
-  p.pb = avg > 12.0 ? 2 : 1;
+  // 16 or 32 pairs per small tile (64 only when forced; measured slower than
+  // the large tiles at 48 pairs per expert)
+  p.pb = avg > 24.0 && a->N % 256 == 0 ? 4 : avg > 12.0 ? 2 : 1;
   p.tile_rows = p.large ? kLargeRows : 16 * p.pb;
   const int64_t nonempty = a->E < p.P ? a->E : p.P;
   p.max_tiles = p.P / p.tile_rows + nonempty;
@@ -178,6 +180,37 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xC07F);  // vmcnt = max, expcnt = max, lgkmcnt = 0
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// s_waitcnt vmcnt(n) for a wave-uniform n known only at run time.
+__device__ __forceinline__ void wait_vmcnt(int n) {  // n uniform, 0..24
+  switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 11: asm volatile("s_waitcnt vmcnt(11)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 13: asm volatile("s_waitcnt vmcnt(13)" ::: "memory"); break;
+    case 14: asm volatile("s_waitcnt vmcnt(14)" ::: "memory"); break;
+    case 15: asm volatile("s_waitcnt vmcnt(15)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 17: asm volatile("s_waitcnt vmcnt(17)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    case 19: asm volatile("s_waitcnt vmcnt(19)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
+    case 21: asm volatile("s_waitcnt vmcnt(21)" ::: "memory"); break;
+    case 22: asm volatile("s_waitcnt vmcnt(22)" ::: "memory"); break;
+    case 23: asm volatile("s_waitcnt vmcnt(23)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+  }
 }
 
 // ============================================================================
@@ -349,6 +382,7 @@ struct GemmParams {
   int nout;              // GEMM 1: N (gate rows; up rows follow); GEMM 2: K
   int topk;
   int col_tiles;         // output-column tiles per pair tile
+  int ct_per_wg;         // column tiles one work-group runs (fm_stream_kernel)
 };
 
 // ---- large tiles -------------------------------------------------------------
@@ -379,15 +413,23 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* s_buf, c
   const int l32 = lane & 31;
   const int hi = lane >> 5;
   const int nst = p.kin / kBK;
-  auto issue = [&](int st) {
+  // A instructions of this wave that hold a pair (rows 32 * wave + 8 * g ..):
+  // the rows past the tile's last pair are never loaded (nor read)
+  const int na = max(0, min(4, (rows - 32 * wave + 7) / 8));
+  // DMA d (0..11) of a stage: A instruction d (d < 4), else B instruction d - 4
+  auto dma = [&](int st, int d) {
     const uint32_t sb = lds0 + uint32_t((st % kStages) * kStage);
-    const uint8_t* ab = abase + int64_t(st) * kRowBytes;
-    const uint8_t* bb = wbase + int64_t(st) * kRowBytes;
+    if (d < 4) {
+      if (d < na)
+        lds_dma(abase + int64_t(st) * kRowBytes, a_off[d], sb + uint32_t((4 * wave + d) * 1024));
+    } else {
+      lds_dma(wbase + int64_t(st) * kRowBytes, b_off[d - 4],
+              sb + uint32_t(kAStage + (8 * wave + d - 4) * 1024));
+    }
+  };
+  auto issue = [&](int st) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) lds_dma(ab, a_off[g], sb + uint32_t((4 * wave + g) * 1024));
-#pragma unroll
-    for (int g = 0; g < 8; ++g)
-      lds_dma(bb, b_off[g], sb + uint32_t(kAStage + (8 * wave + g) * 1024));
+    for (int d = 0; d < 12; ++d) dma(st, d);
   };
 
   f32x16 acc[NRB][2];
@@ -401,14 +443,13 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* s_buf, c
   issue(0);
   if (nst > 1) issue(1);
   for (int st = 0; st < nst; ++st) {
-    // this wave's loads of stage st are complete (12 loads per stage, the
+    // this wave's loads of stage st are complete (na + 8 per stage; the
     // ones of stage st + 1 may still fly), then every wave's are
-    if (st + 1 < nst)
-      asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vmcnt(st + 1 < nst ? na + 8 : 0);
     lds_barrier();
-    if (st + 2 < nst) issue(st + 2);  // into the buffer every wave finished reading
+    // stage st + 2 goes into the buffer every wave finished reading; its 12
+    // DMAs are spread over this stage's MFMAs (one per 2 MFMAs at NRB = 4)
+    const bool more = st + 2 < nst;
     const uint8_t* sa = s_buf + (st % kStages) * kStage;
     const uint8_t* sb = sa + kAStage;
 #pragma unroll
@@ -427,6 +468,13 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, uint8_t* s_buf, c
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb)
           acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[cb], acc[rb][cb], 0, 0, 0);
+        constexpr int kSlots = 4 * NRB;  // MFMA pairs per stage
+        const int slot = kk * NRB + rb;
+        if (more) {
+#pragma unroll
+          for (int d = (slot * 12) / kSlots; d < ((slot + 1) * 12) / kSlots; ++d) dma(st + 2, d);
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the DMAs between the MFMAs
       }
     }
   }
@@ -652,6 +700,192 @@ __global__ void __launch_bounds__(256) fm_skinny_kernel(const GemmParams p) {
   }
 }
 
+// ---- streamed-weight tiles (decode) -------------------------------------------------
+// Same work-group tile as fm_skinny_kernel (16 * PB pairs x 32 weight rows),
+// but every operand reaches the MFMAs through LDS, filled by LDS-DMA in
+// stages of 256 k: one instruction moves two rows' 512 contiguous bytes, so
+// each weight row streams from HBM in long runs. Stages go through a ring of
+// 3-6 buffers (all but one in flight); all waits are explicit (no
+// compiler-tracked load shares the vmcnt counter with the DMAs). Pair rows
+// past the tile's last pair are not loaded. Row r's 16-byte chunk c sits
+// at position c ^ (r & 15) of its 512-byte line, so the 16 rows of a 16x16x32
+// fragment read hit 16 distinct bank groups. The 4 waves split each stage's
+// 8 k-steps (2 each) and add their partial sums through LDS at the end.
+constexpr int kStK = 256;                 // k per stage
+constexpr int kStLine = kStK * 2;         // 512 bytes per row per stage
+
+template <bool kGated, int PB>
+__global__ void __launch_bounds__(256, 1) fm_stream_kernel(const GemmParams p) {
+  constexpr int kRowsW = 32;                        // weight rows per column tile
+  constexpr int kRowsP = 16 * PB;                   // pair rows
+  constexpr int kBuf = (kRowsW + kRowsP) * kStLine; // one stage
+  constexpr int kDmaW = kRowsW / 2 / 4;             // weight DMAs per wave per stage (4)
+  constexpr int kDmaP = kRowsP / 2 / 4;             // pair DMAs per wave per stage (2 PB)
+  // ring depth: as many stages as 144 KiB of LDS hold (6, 4, 3)
+  constexpr int kStBufs = (144 * 1024) / kBuf;
+  static_assert(kStBufs >= 3 && 4 * 2 * PB * 64 * 16 <= kBuf, "ring and reduction fit");
+  __shared__ __attribute__((aligned(1024))) uint8_t s_buf[kStBufs * kBuf];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+
+  // work-group: column tiles ct0 .. ct0 + p.ct_per_wg - 1 of one pair tile,
+  // in one continuous stage pipeline
+  const int wgs_per_tile = (p.col_tiles + p.ct_per_wg - 1) / p.ct_per_wg;
+  const int tile = int(blockIdx.x) / wgs_per_tile;
+  const int ct0 = (int(blockIdx.x) % wgs_per_tile) * p.ct_per_wg;
+  if (tile >= p.tiles[0]) return;
+  const int nct = min(p.ct_per_wg, p.col_tiles - ct0);
+  const int32_t* tl = p.tiles + 4 + 4 * tile;
+  const int e = __builtin_amdgcn_readfirstlane(tl[0]);
+  const int start = __builtin_amdgcn_readfirstlane(tl[1]);
+  const int rows = __builtin_amdgcn_readfirstlane(tl[2]);
+
+  // DMA instruction g of a stage moves rows 2g, 2g + 1 (lane / 32 picks the
+  // row, lane % 32 its chunk position); this wave issues weight instructions
+  // kDmaW * wave + i and pair instructions kDmaP * wave + i. Offsets are for
+  // column tile ct0; a later column tile moves the weight base.
+  const int half = lane >> 5;
+  const int posn = lane & 31;
+  uint32_t w_off[kDmaW];
+#pragma unroll
+  for (int i = 0; i < kDmaW; ++i) {
+    const int r = 2 * (kDmaW * wave + i) + half;  // weight row of the column tile, 0..31
+    int wrow;
+    if (kGated)  // rows 0..15: gate j = 16 ct + r; rows 16..31: up N + 16 ct + r - 16
+      wrow = (r < 16 ? 0 : p.nout - 16) + 16 * ct0 + r;
+    else
+      wrow = 32 * ct0 + r;
+    w_off[i] = uint32_t(int64_t(wrow) * p.kin * 2 + ((posn ^ (r & 15)) * 16));
+  }
+  uint32_t p_off[kDmaP];
+#pragma unroll
+  for (int i = 0; i < kDmaP; ++i) {
+    const int r = 2 * (kDmaP * wave + i) + half;  // pair row of the tile, 0..16 PB - 1
+    const int rr = r < rows ? r : 0;
+    const int64_t arow = kGated ? int64_t(p.sorted[start + rr] / p.topk) : int64_t(start + rr);
+    p_off[i] = uint32_t(arow * p.a_stride * 2 + ((posn ^ (r & 15)) * 16));
+  }
+  // pair instructions of this wave that hold a pair (rows 2 (kDmaP wave + i) ..)
+  const int npd = max(0, min(kDmaP, (rows + 1) / 2 - kDmaP * wave));
+  const int ndma = kDmaW + npd;  // DMAs of this wave per stage
+  const uint8_t* wbase = reinterpret_cast<const uint8_t*>(p.w + int64_t(e) * p.w_estride);
+  const uint8_t* abase = reinterpret_cast<const uint8_t*>(p.a);
+  // bytes between the weight rows of consecutive column tiles
+  const int64_t ct_step = int64_t(kGated ? 16 : 32) * p.kin * 2;
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      uint32_t(reinterpret_cast<uintptr_t>((lds_u8_t*)s_buf)));
+  const int nst = p.kin / kStK;   // stages per column tile
+  const int total = nct * nst;    // stages of the work-group
+  auto issue = [&](int fs) {      // flat stage fs = column tile * nst + stage
+    const int c = fs / nst, st = fs - c * nst;
+    const uint32_t b = lds0 + uint32_t((fs % kStBufs) * kBuf);
+    const uint8_t* wb = wbase + int64_t(c) * ct_step + int64_t(st) * kStLine;
+    const uint8_t* ab = abase + int64_t(st) * kStLine;
+#pragma unroll
+    for (int i = 0; i < kDmaW; ++i)
+      lds_dma(wb, w_off[i], b + uint32_t((kDmaW * wave + i) * 2 * kStLine));
+#pragma unroll
+    for (int i = 0; i < kDmaP; ++i)
+      if (i < npd)
+        lds_dma(ab, p_off[i], b + uint32_t(kRowsW * kStLine + (kDmaP * wave + i) * 2 * kStLine));
+  };
+
+  f32x4 acc[2][PB];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int q = 0; q < PB; ++q) acc[b][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int fs = 0; fs < total && fs < kStBufs - 1; ++fs) issue(fs);
+  for (int fs = 0; fs < total; ++fs) {
+    // this wave's DMAs of stage fs are complete (those of up to two later
+    // stages may fly), then every wave's are
+    wait_vmcnt(ndma * min(kStBufs - 2, total - 1 - fs));
+    lds_barrier();
+    if (fs + kStBufs - 1 < total) issue(fs + kStBufs - 1);  // into the buffer of stage fs - 1
+    const uint8_t* bw = s_buf + (fs % kStBufs) * kBuf;
+    const uint8_t* bp = bw + kRowsW * kStLine;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = (2 * wave + u) * 4 + lg;  // 16-byte chunk of this lane's k within the line
+      bf16x8 wf[2], pf[PB];
+#pragma unroll
+      for (int b = 0; b < 2; ++b) {
+        const int r = 16 * b + li;
+        wf[b] = *reinterpret_cast<const bf16x8*>(bw + r * kStLine + ((c ^ (r & 15)) * 16));
+      }
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        const int r = 16 * q + li;
+        pf[q] = *reinterpret_cast<const bf16x8*>(bp + r * kStLine + ((c ^ (r & 15)) * 16));
+      }
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int q = 0; q < PB; ++q)
+          acc[b][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[b], pf[q], acc[b][q], 0, 0, 0);
+    }
+    if (fs % nst != nst - 1) continue;
+    // ---- last stage of a column tile: add the waves' partial sums (fixed
+    // order: deterministic); wave b < 2 finishes output block b
+    const int ct = ct0 + fs / nst;
+    // the partial sums go through this stage's buffer: every wave is done
+    // with its operands (the barrier below), and the next DMA into it is
+    // issued only after the next stage's barrier
+    lds_barrier();
+    f32x4(*s_red)[2][PB][64] = reinterpret_cast<f32x4(*)[2][PB][64]>(s_buf + (fs % kStBufs) * kBuf);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        s_red[wave][b][q][lane] = acc[b][q];
+        acc[b][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    lds_barrier();
+    if (wave < 2) {
+      const int b = wave;
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        f32x4 sum = s_red[0][b][q][lane];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) sum += s_red[v][b][q][lane];
+        // pair r = 16 q + li, output rows 4 * lg + i of block b
+        const int r = 16 * q + li;
+        if (r >= rows) continue;
+        if (kGated) {
+          // block 0 holds the gate rows, block 1 the up rows of the same j:
+          // wave 0 reads the up partials as well and writes u
+          if (b == 1) continue;
+          f32x4 up = s_red[0][1][q][lane];
+#pragma unroll
+          for (int v = 1; v < 4; ++v) up += s_red[v][1][q][lane];
+          bf16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float g = bf16r(silu(bf16r(sum[i])));
+            o[i] = static_cast<__bf16>(bf16r(up[i]) * g);
+          }
+          *reinterpret_cast<bf16x4*>(p.out + int64_t(start + r) * p.out_stride + 16 * ct +
+                                     4 * lg) = o;
+        } else {
+          const int pair = p.sorted[start + r];
+          const float wt = p.wts[pair];
+          bf16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = static_cast<__bf16>(bf16r(sum[i]) * wt);
+          *reinterpret_cast<bf16x4*>(p.out + int64_t(pair) * p.out_stride + 32 * ct + 16 * b +
+                                     4 * lg) = o;
+        }
+      }
+    }
+    // the buffer is next written by the DMA of a later stage, issued after
+    // a barrier that every wave reaches only after reading it here
+  }
+}
+
 // ============================================================================
 // final sum over each token's experts
 // ============================================================================
@@ -761,11 +995,34 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
     g1.col_tiles = int(a->N / 16);
     g2.col_tiles = int(a->K / 32);
   }
-  const unsigned grid1 = unsigned(pl.max_tiles * g1.col_tiles);
-  const unsigned grid2 = unsigned(pl.max_tiles * g2.col_tiles);
+  // small tiles stream their weights through LDS when both reductions are
+  // whole 256-wide stages, else straight into registers
+  const bool streamed = !pl.large && a->N % kStK == 0;  // (K % 256 == 0 always holds)
+  g1.ct_per_wg = g2.ct_per_wg = 1;
+  if (streamed) {
+    // a streaming work-group runs several column tiles in one pipeline, so its
+    // start (tile table -> pair list -> first DMA) is paid once per
+    // several: about 1024 work-groups per launch, whole column tiles each
+    for (GemmParams* g : {&g1, &g2}) {
+      int c = 1;
+      while (c * 2 <= g->col_tiles && pl.max_tiles * (g->col_tiles / (c * 2)) >= 1024) c *= 2;
+      g->ct_per_wg = c;
+    }
+  }
+  auto grid_of = [&](const GemmParams& g) {
+    return unsigned(pl.max_tiles * ((g.col_tiles + g.ct_per_wg - 1) / g.ct_per_wg));
+  };
+  const unsigned grid1 = grid_of(g1);
+  const unsigned grid2 = grid_of(g2);
   if (!mark(FM_KERNEL_GATEUP, 0)) return FM_EHIP;
   if (pl.large)
     hipLaunchKernelGGL(fm_gemm_kernel<true>, dim3(grid1), dim3(256), 0, stream, g1);
+  else if (streamed && pl.pb == 1)
+    hipLaunchKernelGGL((fm_stream_kernel<true, 1>), dim3(grid1), dim3(256), 0, stream, g1);
+  else if (streamed && pl.pb == 2)
+    hipLaunchKernelGGL((fm_stream_kernel<true, 2>), dim3(grid1), dim3(256), 0, stream, g1);
+  else if (streamed)
+    hipLaunchKernelGGL((fm_stream_kernel<true, 4>), dim3(grid1), dim3(256), 0, stream, g1);
   else if (pl.pb == 1)
     hipLaunchKernelGGL((fm_skinny_kernel<true, 1>), dim3(grid1), dim3(256), 0, stream, g1);
   else
@@ -774,6 +1031,12 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   if (!mark(FM_KERNEL_DOWN, 0)) return FM_EHIP;
   if (pl.large)
     hipLaunchKernelGGL(fm_gemm_kernel<false>, dim3(grid2), dim3(256), 0, stream, g2);
+  else if (streamed && pl.pb == 1)
+    hipLaunchKernelGGL((fm_stream_kernel<false, 1>), dim3(grid2), dim3(256), 0, stream, g2);
+  else if (streamed && pl.pb == 2)
+    hipLaunchKernelGGL((fm_stream_kernel<false, 2>), dim3(grid2), dim3(256), 0, stream, g2);
+  else if (streamed)
+    hipLaunchKernelGGL((fm_stream_kernel<false, 4>), dim3(grid2), dim3(256), 0, stream, g2);
   else if (pl.pb == 1)
     hipLaunchKernelGGL((fm_skinny_kernel<false, 1>), dim3(grid2), dim3(256), 0, stream, g2);
   else
