@@ -469,7 +469,7 @@ def moe_cpu_baseline(hidden, w1, w2, score, topk, target_s=3.0, runs=3):
                        f"(oracle/fused_moe_ref.py, routed tokens only), {threads} threads")}
 
 
-def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
+def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
     """One record per track-03 workload: µs/call of the drop-in
     (submission.fused_moe), algorithmic TFLOP/s (6 N K flop per routed
     (token, expert) pair: 4 N K gate-up, 2 N K down), compulsory HBM bytes
@@ -480,7 +480,9 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     submission.load_extension()
     recs = []
     first = True
-    for label, M, K, N, E, topk in MOE_WORKLOADS:
+    for i_w, (label, M, K, N, E, topk) in enumerate(MOE_WORKLOADS):
+        if only is not None and i_w != only:
+            continue
         sets = [moe_inputs(M, K, N, E, seed=100 + i) for i in range(nsets)]
         fn = lambda h, a1, a2, sc, _s: submission.fused_moe(h, a1, a2, sc, topk)  # noqa: E731
         tsets = [s for s in sets]
@@ -608,6 +610,8 @@ def main():
                     help="time the reference harness's ten contest shapes instead")
     ap.add_argument("--moe", action="store_true",
                     help="time track 03's fused_moe on its eight workloads instead")
+    ap.add_argument("--moe-workload", type=int, default=None,
+                    help="with --moe: only workload i (0..7) of track-03/workloads.py")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy of known size (PMC byte scaling)")
     args = ap.parse_args()
@@ -632,7 +636,8 @@ def main():
             print(json.dumps(rec), flush=True)
         return
     if args.moe:
-        for rec in bench_moe(args.steps, args.warmup, args.sets, not args.no_cpu, args.settle):
+        for rec in bench_moe(args.steps, args.warmup, args.sets, not args.no_cpu, args.settle,
+                             args.moe_workload):
             print(json.dumps(rec), flush=True)
         return
     if args.all:
