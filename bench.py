@@ -75,11 +75,19 @@ KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel"
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the same
-# counters read for a plain copy of known size (bench.py --copy-calibration:
-# FETCH_SIZE x 2.0000, WRITE_SIZE x 1.0000). Commands and raw figures:
-# profiles/<kernel>_<workload>_pmc.txt. Measured for the kernels as built.
-TRAFFIC = {"causal_prefill": 206198454, "high_locality": 232269823,
-           "long_context": 2125966694, "decode": 80157116, "plumbing": 17494372}
+# counters read for a plain copy of known size (bench.py --copy-calibration).
+# profiles/traffic.json holds the figure per workload, with the commit whose
+# kernels were profiled and the summary (command, raw figures) it came from.
+TRAFFIC_JSON = os.path.join(REPO, "profiles", "traffic.json")
+
+
+def traffic_of(workload):
+    """(bytes per launch, commit, profile) of a workload's dominant kernel, or None."""
+    try:
+        rec = json.load(open(TRAFFIC_JSON))["workloads"][workload]
+    except (OSError, KeyError, ValueError):
+        return None
+    return rec["bytes_per_launch"], rec.get("commit"), rec.get("profile")
 
 
 def algorithmic(idx_cpu: torch.Tensor, b, m):
@@ -233,7 +241,10 @@ def roofline(name, flops, compulsory, times):
         ach = compulsory * share / t / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
                 "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4)}
-    roof["traffic"] = TRAFFIC.get(name)
+    tr = traffic_of(name)
+    roof["traffic"] = tr[0] if tr else None
+    if tr:
+        roof["traffic_commit"], roof["traffic_profile"] = tr[1], tr[2]
     roof["kernel"] = KERNEL_NAMES[dom]
     roof["kernel_us"] = round(times[dom] * 1e3, 2)
     roof["work_share"] = round(share, 4)
@@ -512,7 +523,11 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
             ach = b_dom / td / 1e9
             roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
                     "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4)}
-        roof.update({"traffic": None, "kernel": MOE_KERNEL_NAMES[dom],
+        tr = traffic_of(f"moe{MOE_WORKLOADS.index((label, M, K, N, E, topk))}") \
+            if dom == "gateup" else None
+        if tr:
+            roof.update({"traffic_commit": tr[1], "traffic_profile": tr[2]})
+        roof.update({"traffic": tr[0] if tr else None, "kernel": MOE_KERNEL_NAMES[dom],
                      "kernel_us": round(times[dom] * 1e3, 2),
                      "kernel_us_all": {MOE_KERNEL_NAMES[k]: round(v * 1e3, 2)
                                        for k, v in times.items()}})

@@ -56,8 +56,13 @@ def test_algorithmic_work():
 
 
 def test_tables():
-    assert set(bench.TRAFFIC) == set(wl.CONFIGS)
-    assert all(v > 0 for v in bench.TRAFFIC.values())
+    # traffic of every BASELINE config and every track-03 workload comes from
+    # a committed profile summary that names the commit it measured
+    for name in list(wl.CONFIGS) + [f"moe{i}" for i in range(len(bench.MOE_WORKLOADS))]:
+        tr = bench.traffic_of(name)
+        assert tr is not None and tr[0] > 0, name
+        assert tr[1] and os.path.exists(os.path.join(bench.REPO, tr[2])), name
+    assert len(bench.MOE_WORKLOADS) == 8
     shapes = {(d, p) for _, d, _, p, _ in bench.HC_WORKLOADS}
     assert shapes == {((1, 1), (1, 16384)), ((16, 1), (16, 4096)), ((64, 1), (64, 1024))}
     assert [n for n, *_ in bench.HC_WORKLOADS] == ["16k-1k-1", "4k-1k-16", "1k-1k-64", "1k-1-64"]
