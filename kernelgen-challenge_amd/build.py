@@ -101,7 +101,7 @@ def build_torch_ext(verbose=False):
     cmd += [os.path.join(CSRC, "sa_torch.cpp"), "-o", tmp]
     cmd += [f"-L{p}" for p in libdirs] + [f"-L{LIB_DIR}", f"-L{ROCM}/lib"]
     cmd += ["-lsparse_attn_gfx950", "-lhc_sinkhorn_gfx950", "-lfused_moe_gfx950", "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
-            "-ltorch_hip", "-lamdhip64", "-Wl,-rpath,$ORIGIN"]
+            "-ltorch_hip", "-ltorch_python", "-lamdhip64", "-Wl,-rpath,$ORIGIN"]
     cmd += [f"-Wl,-rpath,{p}" for p in libdirs]
     _run(cmd, verbose)
     os.replace(tmp, TORCH_EXT)

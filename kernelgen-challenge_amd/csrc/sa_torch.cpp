@@ -14,6 +14,7 @@
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
+#include <torch/csrc/utils/pybind.h>
 #include <torch/library.h>
 
 #include <mutex>
@@ -112,7 +113,7 @@ std::tuple<at::Tensor, at::Tensor> forward(const at::Tensor& q, const at::Tensor
                     q.sizes());
 
   const c10::DeviceGuard guard(q.device());
-  const at::Tensor sink_c = attn_sink.contiguous();
+  const at::Tensor sink_c = attn_sink.is_contiguous() ? attn_sink : attn_sink.contiguous();
   at::Tensor o = at::empty({b, m, h, d}, q.options());
   at::Tensor lse;
 
@@ -309,16 +310,18 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> hc_split_sinkhorn_op(
   TORCH_CHECK_VALUE(sinkhorn_iters >= INT32_MIN && sinkhorn_iters <= INT32_MAX,
                     "sinkhorn_iters out of range");
   const c10::DeviceGuard guard(mixes.device());
-  at::Tensor x = mixes.contiguous();
+  // (each tensor op below goes through the dispatcher: a small call's host
+  // time is mostly these, so inputs that are already fine are not touched)
+  at::Tensor x = mixes.is_contiguous() ? mixes : mixes.contiguous();
   if ((reinterpret_cast<uintptr_t>(x.data_ptr()) & 15u) != 0) x = x.clone();  // 16-byte rows
-  const at::Tensor sc = hc_scale.contiguous();
-  const at::Tensor bs = hc_base.contiguous();
+  const at::Tensor sc = hc_scale.is_contiguous() ? hc_scale : hc_scale.contiguous();
+  const at::Tensor bs = hc_base.is_contiguous() ? hc_base : hc_base.contiguous();
   const int64_t b = mixes.size(0), s = mixes.size(1), n = b * s;
   // One allocation, three contiguous outputs carved from it (pre, post, comb)
   at::Tensor out = at::empty({24 * n}, x.options());
-  at::Tensor pre = out.narrow(0, 0, 4 * n).view({b, s, 4});
-  at::Tensor post = out.narrow(0, 4 * n, 4 * n).view({b, s, 4});
-  at::Tensor comb = out.narrow(0, 8 * n, 16 * n).view({b, s, 4, 4});
+  at::Tensor pre = out.as_strided({b, s, 4}, {4 * s, 4, 1}, 0);
+  at::Tensor post = out.as_strided({b, s, 4}, {4 * s, 4, 1}, 4 * n);
+  at::Tensor comb = out.as_strided({b, s, 4, 4}, {16 * s, 16, 4, 1}, 8 * n);
   hc_args a{};
   a.mixes = x.data_ptr<float>();
   a.scale = sc.data_ptr<float>();
@@ -441,4 +444,32 @@ TORCH_LIBRARY_IMPL(sa_amd, CUDA, m) {
 // No tensor argument: registered for every dispatch key.
 TORCH_LIBRARY_IMPL(sa_amd, CatchAll, m) {
   m.impl("index_error_flag_address", &index_error_flag_address);
+}
+
+// The same operators as plain Python functions of this module (sa_torch_ext),
+// for the drop-ins: a call through torch.ops boxes every argument and result
+// for the dispatcher, which costs several microseconds, more than the whole
+// kernel of a small call. torch.ops.sa_amd.* stays registered for callers
+// that need the dispatcher. Argument names and defaults follow the schemas
+// above.
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  namespace py = pybind11;
+  using py::arg;
+  m.def("sparse_attn_fwd", &sparse_attn_fwd, arg("q"), arg("kv"), arg("attn_sink"),
+        arg("topk_idxs"), arg("scale"), arg("err") = py::none(), arg("flags") = 0,
+        arg("deferred_check") = false);
+  m.def("sparse_attn_fwd_lse", &sparse_attn_fwd_lse, arg("q"), arg("kv"), arg("attn_sink"),
+        arg("topk_idxs"), arg("scale"), arg("err") = py::none(), arg("flags") = 0,
+        arg("deferred_check") = false);
+  m.def("sparse_attn_fwd_planned", &sparse_attn_fwd_planned, arg("q"), arg("kv"),
+        arg("attn_sink"), arg("topk_idxs"), arg("scale"), arg("plan"), arg("err") = py::none(),
+        arg("flags") = 0, arg("deferred_check") = false);
+  m.def("sparse_attn_fwd_lse_planned", &sparse_attn_fwd_lse_planned, arg("q"), arg("kv"),
+        arg("attn_sink"), arg("topk_idxs"), arg("scale"), arg("plan"), arg("err") = py::none(),
+        arg("flags") = 0, arg("deferred_check") = false);
+  m.def("hc_split_sinkhorn", &hc_split_sinkhorn_op, arg("mixes"), arg("hc_scale"),
+        arg("hc_base"), arg("hc_mult") = 4, arg("sinkhorn_iters") = 20, arg("eps") = 1e-6,
+        arg("flags") = 0);
+  m.def("fused_moe", &fused_moe_op, arg("hidden"), arg("w1"), arg("w2"), arg("score"),
+        arg("topk"), arg("renormalize") = false, arg("flags") = 0);
 }

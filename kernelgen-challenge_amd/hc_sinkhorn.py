@@ -22,14 +22,15 @@ __all__ = ["hc_split_sinkhorn", "FLAG_LANES16", "FLAG_LANES1"]
 FLAG_LANES16 = 1
 FLAG_LANES1 = 2
 
-_op = None  # torch.ops.sa_amd.hc_split_sinkhorn once the extension is loaded
+_op = None  # the extension's hc_split_sinkhorn once it is loaded
 
 
 def _load():
     global _op
     from submission import load_extension  # lazy: submission re-exports this module
-    load_extension()
-    _op = torch.ops.sa_amd.hc_split_sinkhorn
+    # the module function, not torch.ops.sa_amd.hc_split_sinkhorn: the same
+    # operator without the dispatcher's per-call boxing
+    _op = load_extension().hc_split_sinkhorn
     return _op
 
 

@@ -25,14 +25,15 @@ __all__ = ["fused_moe", "FLAG_LARGE_TILES", "FLAG_SMALL_TILES"]
 FLAG_LARGE_TILES = 1
 FLAG_SMALL_TILES = 2
 
-_op = None  # torch.ops.sa_amd.fused_moe once the extension is loaded
+_op = None  # the extension's fused_moe once it is loaded
 
 
 def _load():
     global _op
     from submission import load_extension  # lazy: submission re-exports this module
-    load_extension()
-    _op = torch.ops.sa_amd.fused_moe
+    # the module function, not torch.ops.sa_amd.fused_moe: the same operator
+    # without the dispatcher's per-call boxing
+    _op = load_extension().fused_moe
     return _op
 
 

@@ -5,8 +5,10 @@ Same module name and signature as the reference entry point
 ``sys.path`` and ``from submission import sparse_attn``.
 
 The call runs the hand-written gfx950 HIP kernels through the operator
-``torch.ops.sa_amd.sparse_attn_fwd`` (``csrc/sa_torch.cpp``), which calls the
-C-ABI ``sa_forward`` (``include/sparse_attn.h``) on torch's current stream.
+``sparse_attn_fwd`` of the in-tree extension ``sa_torch_ext``
+(``csrc/sa_torch.cpp``; called as a Python function of that module, and also
+registered as ``torch.ops.sa_amd.sparse_attn_fwd``), which calls the C-ABI
+``sa_forward`` (``include/sparse_attn.h``) on torch's current stream.
 There is no other code path: if the extension is not built, or the tensors are
 not on a GPU, the call raises.
 
@@ -29,6 +31,7 @@ environment variable ``SPARSE_ATTN_CHECK``):
 from __future__ import annotations
 
 import ctypes
+import importlib.util
 import os
 import threading
 
@@ -44,6 +47,7 @@ _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 _EXT_PATH = os.path.join(_PKG_DIR, "lib", "sa_torch_ext.so")
 _lock = threading.Lock()
 _loaded = False
+_ext = None  # sa_torch_ext as a Python module: the operators without the dispatcher
 _CHECK_MODES = ("deferred", "sync", "off")
 
 
@@ -70,20 +74,26 @@ def extension_path() -> str:
     return _EXT_PATH
 
 
-def load_extension() -> None:
-    """Load the in-tree operator library (idempotent). Raises if it is missing."""
-    global _loaded
+def load_extension():
+    """Load the in-tree operator library (idempotent) and return it as a
+    Python module. Raises if it is missing."""
+    global _loaded, _ext
     if _loaded:
-        return
+        return _ext
     with _lock:
         if _loaded:
-            return
+            return _ext
         if not os.path.exists(_EXT_PATH):
             raise RuntimeError(
                 "sparse_attn: the gfx950 extension is not built "
                 f"({_EXT_PATH} missing); run `python kernelgen-challenge_amd/build.py`")
-        torch.ops.load_library(_EXT_PATH)
+        torch.ops.load_library(_EXT_PATH)  # torch.ops.sa_amd.*
+        spec = importlib.util.spec_from_file_location("sa_torch_ext", _EXT_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _ext = mod
         _loaded = True
+        return _ext
 
 
 def set_index_check(mode) -> None:
@@ -109,6 +119,7 @@ def _err_flag(device):
         with _lock:
             f = _err_flags.get(i)
             if f is None:
+                load_extension()
                 addr = torch.ops.sa_amd.index_error_flag_address(i)
                 f = _err_flags[i] = ctypes.c_int32.from_address(addr)
     return f
@@ -149,7 +160,6 @@ def _checked_inputs(q, kv, attn_sink, topk_idxs):
         raise ValueError("expected kv [b, kv_len, d], attn_sink [h], topk_idxs [b, m, topk]")
     if not (q.is_cuda and kv.is_cuda and attn_sink.is_cuda and topk_idxs.is_cuda):
         raise ValueError("sparse_attn runs on the GPU only; move all inputs to the device")
-    load_extension()
     # Same input handling as track-01/submission.py:995-998.
     return q.contiguous(), kv.contiguous(), attn_sink.contiguous(), topk_idxs.contiguous()
 
@@ -245,13 +255,13 @@ def sparse_attn(q, kv, attn_sink, topk_idxs, scale, plan=None):
     """
     q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
     err, deferred = _check_args(q.device)
+    ext = _ext or load_extension()
     if plan is None:
-        o = torch.ops.sa_amd.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags,
-                                             deferred)
+        o = ext.sparse_attn_fwd(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags, deferred)
     else:
         plan._check(topk_idxs, _plan_key(q, kv_c, topk_idxs))
-        o = torch.ops.sa_amd.sparse_attn_fwd_planned(q_c, kv_c, sink_c, plan.idx, float(scale),
-                                                     plan.workspace, err, _flags, deferred)
+        o = ext.sparse_attn_fwd_planned(q_c, kv_c, sink_c, plan.idx, float(scale),
+                                        plan.workspace, err, _flags, deferred)
     _raise_if_bad_index(err, kv.shape[1])
     return o
 
@@ -269,12 +279,13 @@ def sparse_attn_with_lse(q, kv, attn_sink, topk_idxs, scale, plan=None):
     """
     q_c, kv_c, sink_c, idx_c = _checked_inputs(q, kv, attn_sink, topk_idxs)
     err, deferred = _check_args(q.device)
+    ext = _ext or load_extension()
     if plan is None:
-        o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse(q_c, kv_c, sink_c, idx_c, float(scale),
-                                                      err, _flags, deferred)
+        o, lse = ext.sparse_attn_fwd_lse(q_c, kv_c, sink_c, idx_c, float(scale), err, _flags,
+                                         deferred)
     else:
         plan._check(topk_idxs, _plan_key(q, kv_c, topk_idxs))
-        o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse_planned(
+        o, lse = ext.sparse_attn_fwd_lse_planned(
             q_c, kv_c, sink_c, plan.idx, float(scale), plan.workspace, err, _flags, deferred)
     _raise_if_bad_index(err, kv.shape[1])
     return o, lse
