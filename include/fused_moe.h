@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FM_ABI_VERSION 1
+#define FM_ABI_VERSION 2
 
 enum {
   FM_OK = 0,
@@ -44,7 +44,9 @@ enum {
 /* fm_args.flags (0 = let the library choose). */
 enum {
   FM_FLAG_LARGE_TILES = 1u,  /* 128-pair tiles whatever the tokens per expert */
-  FM_FLAG_SMALL_TILES = 2u   /* 16-pair weight-streaming tiles */
+  FM_FLAG_SMALL_TILES = 2u,  /* 16-pair weight-streaming tiles */
+  FM_FLAG_BIG_TILES = 4u     /* (ABI version 2) 256-pair tiles, 8 waves per work-group;
+                                by default once experts average 256 pairs */
 };
 
 typedef struct fm_args {

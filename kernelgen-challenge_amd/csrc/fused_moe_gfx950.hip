@@ -61,6 +61,7 @@ struct Plan {
   int64_t P;            // pairs = M * topk
   int tile_rows;        // pairs per tile
   bool large;           // fm_gemm_kernel (else fm_skinny_kernel)
+  bool big;             // large, with 256-pair tiles: fm_gemm_big_kernel
   int pb;               // small tiles: 16-pair blocks per tile (1, 2 or 4)
   int64_t max_tiles;    // upper bound on sum_e ceil(count_e / tile_rows)
   size_t ids_off, wts_off, eoff_off, sorted_off, tiles_off, inter_off, y_off, bytes;
@@ -72,16 +73,23 @@ Plan make_plan(const fm_args* a) {
   Plan p{};
   p.P = a->M * a->topk;
   const double avg = double(p.P) / double(a->E);  // pairs per expert on average
-  if (a->flags & FM_FLAG_LARGE_TILES)
+  if (a->flags & (FM_FLAG_LARGE_TILES | FM_FLAG_BIG_TILES))
     p.large = true;
   else if (a->flags & FM_FLAG_SMALL_TILES)
     p.large = false;
   else
     p.large = avg > 24.0;
+  // 256-pair tiles once an expert's pairs fill them on average and their
+  // gate-up GEMM still has a work-group for each of MI355X's 256 CUs
+  // (P / 256 pair tiles x N / 128 column tiles); fewer, and the 128-pair
+  // tiles' larger grid is faster (measured at M = 1024, 2048 with E = 8)
+  p.big = (a->flags & FM_FLAG_BIG_TILES) != 0 ||
+          ((a->flags & FM_FLAG_LARGE_TILES) == 0 && p.large && avg >= 256.0 &&
+           (p.P / 256) * (a->N / 128) >= 256);
   // 16 or 32 pairs per small tile (64 only when forced; measured slower than
   // the large tiles at 48 pairs per expert)
   p.pb = avg > 24.0 && a->N % 256 == 0 ? 4 : avg > 12.0 ? 2 : 1;
-  p.tile_rows = p.large ? kLargeRows : 16 * p.pb;
+  p.tile_rows = p.big ? 256 : p.large ? kLargeRows : 16 * p.pb;
   const int64_t nonempty = a->E < p.P ? a->E : p.P;
   p.max_tiles = p.P / p.tile_rows + nonempty;
   size_t off = 0;
@@ -107,9 +115,10 @@ int validate(const fm_args* a) {
   if (a->topk > a->E) return FM_EINVAL;
   if (a->E > kMaxExperts || a->topk > kMaxTopk) return FM_EUNSUPPORTED;
   if (a->K % kLargeCols != 0 || a->N % (kLargeCols / 2) != 0) return FM_EUNSUPPORTED;
-  if ((a->flags & ~uint32_t(FM_FLAG_LARGE_TILES | FM_FLAG_SMALL_TILES)) != 0 ||
-      (a->flags & FM_FLAG_LARGE_TILES && a->flags & FM_FLAG_SMALL_TILES))
-    return FM_EINVAL;
+  const uint32_t tile_flags = a->flags & (FM_FLAG_LARGE_TILES | FM_FLAG_SMALL_TILES |
+                                          FM_FLAG_BIG_TILES);
+  if ((a->flags & ~tile_flags) != 0 || (tile_flags & (tile_flags - 1)) != 0)
+    return FM_EINVAL;  // unknown bits, or more than one tile choice
   if (a->M == 0) return FM_OK;
   if (!a->hidden || !a->w1 || !a->w2 || !a->score || !a->out) return FM_EINVAL;
   auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
@@ -578,6 +587,207 @@ __global__ void __launch_bounds__(256, 1) fm_gemm_kernel(const GemmParams p) {
 #undef FM_TILE
 }
 
+// ---- big tiles (many pairs per expert) -----------------------------------------------
+// Work-group: 256 pairs x 256 weight rows, 8 waves, two per SIMD. Wave w
+// computes pair half w >> 2 (128 pairs, 4 row blocks) against weight quarter
+// w & 3 (64 rows, 2 column blocks): the 128-pair tile's per-wave shape, with
+// each weight fragment now feeding 256 pairs and each pair fragment 256 rows,
+// so a stage moves 128 flop per byte into LDS (85 for the 128-pair tile), and
+// the second wave on each SIMD issues MFMAs while the first waits for its
+// fragment reads. K streams in 32-wide stages through a 4-deep ring (32 KiB
+// per stage: A 256 rows, then B 256 rows, of 64 bytes): three stages are in
+// flight while one is read. Row r's 16-byte chunk c sits at c ^ ((r >> 2) & 3):
+// 16 consecutive rows of one chunk (a fragment read's LDS cycle) then hit 16
+// distinct groups of 4 banks. Each wave moves A rows 32w..32w+31 and B rows
+// 32w..32w+31 of every stage (two 16-row LDS-DMA instructions each; A rows
+// past the tile's last pair are skipped).
+constexpr int kBigRows = 256;                        // pairs per tile
+constexpr int kBigBK = 32;                           // k per stage
+constexpr int kBigStages = 4;
+constexpr int kBigRowBytes = kBigBK * 2;             // 64
+constexpr int kBigAStage = kBigRows * kBigRowBytes;  // 16 KiB
+constexpr int kBigStage = 2 * kBigAStage;            // A then B (256 weight rows)
+static_assert(kLargeCols == 256, "the big tile's weight rows are the large tile's");
+
+__device__ __forceinline__ int swz4(int row, int chunk) { return chunk ^ ((row >> 2) & 3); }
+
+// The K loop and epilogue of one wave's share of a big tile; NRB = the 32-pair
+// row blocks of the wave's half holding pairs (0: DMAs and barriers only).
+template <bool kGated, int NRB>
+__device__ __forceinline__ void big_tile(const GemmParams& p, const uint8_t* s_buf,
+                                         const int* s_pair, const float* s_wt,
+                                         const uint8_t* abase, const uint8_t* wbase,
+                                         const uint32_t (&a_off)[2], const uint32_t (&b_off)[2],
+                                         uint32_t lds0, int na, int start, int rows, int ct) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ph = wave >> 2;  // pair half
+  const int wq = wave & 3;   // weight quarter
+  const int l32 = lane & 31;
+  const int hi = lane >> 5;
+  const int nst = p.kin / kBigBK;
+  const int per_stage = na + 2;  // this wave's DMAs per stage
+  auto issue = [&](int st) {
+    const uint32_t sb = lds0 + uint32_t((st % kBigStages) * kBigStage);
+    const int64_t k0 = int64_t(st) * kBigRowBytes;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+      if (g < na) lds_dma(abase + k0, a_off[g], sb + uint32_t((2 * wave + g) * 1024));
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+      lds_dma(wbase + k0, b_off[g], sb + uint32_t(kBigAStage + (2 * wave + g) * 1024));
+  };
+
+  f32x16 acc[NRB > 0 ? NRB : 1][2];
+#pragma unroll
+  for (int rb = 0; rb < (NRB > 0 ? NRB : 1); ++rb)
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[rb][cb][i] = 0.f;
+
+  for (int st = 0; st < kBigStages - 1 && st < nst; ++st) issue(st);
+  for (int st = 0; st < nst; ++st) {
+    // this wave's loads of stage st are complete (those of the up to two
+    // stages issued after it may still fly), then every wave's are
+    wait_vmcnt(min(nst - 1, st + kBigStages - 2) - st > 0
+                   ? (min(nst - 1, st + kBigStages - 2) - st) * per_stage
+                   : 0);
+    lds_barrier();
+    // the buffer of stage st - 1, which every wave has finished reading
+    if (st + kBigStages - 1 < nst) issue(st + kBigStages - 1);
+    if constexpr (NRB > 0) {
+      const uint8_t* sa = s_buf + (st % kBigStages) * kBigStage;
+      const uint8_t* sb = sa + kBigAStage;
+      // both k-steps' fragments first: the second's reads fly under the
+      // first's MFMAs
+      bf16x8 bf[2][2], af[2][NRB];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int c = 2 * kk + hi;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int lr = 64 * wq + 32 * cb + l32;
+          bf[kk][cb] = *reinterpret_cast<const bf16x8*>(sb + lr * kBigRowBytes + swz4(lr, c) * 16);
+        }
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb) {
+          const int r = 128 * ph + 32 * rb + l32;
+          af[kk][rb] = *reinterpret_cast<const bf16x8*>(sa + r * kBigRowBytes + swz4(r, c) * 16);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk][rb], bf[kk][cb],
+                                                                   acc[rb][cb], 0, 0, 0);
+    }
+  }
+
+  // epilogue: lane holds column l32 of each column block and pair rows
+  // 128 * ph + 32 * rb + 8 * a + 4 * hi + b in register 4 * a + b
+  if constexpr (NRB > 0) {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int r = 128 * ph + 32 * rb + 8 * a + 4 * hi + b;
+          if (r >= rows) continue;
+          const int ri = 4 * a + b;
+          if (kGated) {
+            const float g = bf16r(silu(bf16r(acc[rb][0][ri])));
+            const float u = bf16r(acc[rb][1][ri]) * g;
+            const int j = ct * (kLargeCols / 2) + 32 * wq + l32;
+            p.out[int64_t(start + r) * p.out_stride + j] = static_cast<__bf16>(u);
+          } else {
+            const int pair = s_pair[r];
+            const float w = s_wt[r];
+#pragma unroll
+            for (int cb = 0; cb < 2; ++cb) {
+              const int f = ct * kLargeCols + 64 * wq + 32 * cb + l32;
+              p.out[int64_t(pair) * p.out_stride + f] =
+                  static_cast<__bf16>(bf16r(acc[rb][cb][ri]) * w);
+            }
+          }
+        }
+    }
+  }
+}
+
+template <bool kGated>
+__global__ void __launch_bounds__(512, 1) fm_gemm_big_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t s_buf[kBigStages * kBigStage];
+  __shared__ int s_pair[kBigRows];
+  __shared__ float s_wt[kBigRows];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  const int tile = int(blockIdx.x) / p.col_tiles;
+  const int ct = int(blockIdx.x) % p.col_tiles;
+  if (tile >= p.tiles[0]) return;
+  const int32_t* tl = p.tiles + 4 + 4 * tile;
+  const int e = __builtin_amdgcn_readfirstlane(tl[0]);
+  const int start = __builtin_amdgcn_readfirstlane(tl[1]);
+  const int rows = __builtin_amdgcn_readfirstlane(tl[2]);
+
+  if (tid < kBigRows) {
+    const int r = tid < rows ? tid : 0;
+    const int pair = p.sorted[start + r];
+    s_pair[tid] = pair;
+    if (!kGated) s_wt[tid] = p.wts[pair];
+  }
+  __syncthreads();
+
+  // Per-lane DMA sources: instruction g of this wave moves LDS rows
+  // 32 * wave + 16 * g + lane / 4, lane & 3 being the chunk position there.
+  const int sub = lane >> 2;
+  const int pos = lane & 3;
+  uint32_t a_off[2], b_off[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int r = 32 * wave + 16 * g + sub;
+    const int c = swz4(r, pos);  // the chunk whose swizzled position is `pos`
+    const int64_t arow =
+        kGated ? int64_t(s_pair[r] / p.topk) : int64_t(start + (r < rows ? r : 0));
+    a_off[g] = uint32_t(arow * p.a_stride * 2 + c * 16);
+    // weight row of LDS row r: weight quarter r >> 6, column block (r >> 5) & 1
+    int wrow;
+    if (kGated)  // gate rows j, up rows N + j, j = ct * 128 + 32 * (r >> 6) + (r & 31)
+      wrow = (((r >> 5) & 1) ? p.nout : 0) + ct * (kLargeCols / 2) + 32 * (r >> 6) + (r & 31);
+    else         // features f = ct * 256 + r
+      wrow = ct * kLargeCols + r;
+    b_off[g] = uint32_t(int64_t(wrow) * p.kin * 2 + c * 16);
+  }
+  // A instructions of this wave that hold a pair
+  const int na = max(0, min(2, (rows - 32 * wave + 15) / 16));
+  const uint8_t* abase = reinterpret_cast<const uint8_t*>(p.a);
+  const uint8_t* wbase = reinterpret_cast<const uint8_t*>(p.w + int64_t(e) * p.w_estride);
+  const uint32_t lds0 = __builtin_amdgcn_readfirstlane(
+      uint32_t(reinterpret_cast<uintptr_t>((lds_u8_t*)s_buf)));
+
+  // 32-pair row blocks of this wave's half that hold pairs
+  const int nrb = max(0, min(4, (rows - 128 * (wave >> 2) + 31) / 32));
+#define FM_BIG(n)                                                                          \
+  big_tile<kGated, n>(p, s_buf, s_pair, s_wt, abase, wbase, a_off, b_off, lds0, na, start, \
+                      rows, ct)
+  switch (nrb) {
+    case 0: FM_BIG(0); break;
+    case 1: FM_BIG(1); break;
+    case 2: FM_BIG(2); break;
+    case 3: FM_BIG(3); break;
+    default: FM_BIG(4); break;
+  }
+#undef FM_BIG
+}
+
 // ---- skinny tiles (few pairs per expert) ------------------------------------------
 // Work-group: one tile of up to 16 * PB pairs x 16 output rows (gated: 16
 // gate rows j and the 16 up rows N + j; else 32 features in two blocks).
@@ -1015,7 +1225,9 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   const unsigned grid1 = grid_of(g1);
   const unsigned grid2 = grid_of(g2);
   if (!mark(FM_KERNEL_GATEUP, 0)) return FM_EHIP;
-  if (pl.large)
+  if (pl.big)
+    hipLaunchKernelGGL(fm_gemm_big_kernel<true>, dim3(grid1), dim3(512), 0, stream, g1);
+  else if (pl.large)
     hipLaunchKernelGGL(fm_gemm_kernel<true>, dim3(grid1), dim3(256), 0, stream, g1);
   else if (streamed && pl.pb == 1)
     hipLaunchKernelGGL((fm_stream_kernel<true, 1>), dim3(grid1), dim3(256), 0, stream, g1);
@@ -1029,7 +1241,9 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
     hipLaunchKernelGGL((fm_skinny_kernel<true, 2>), dim3(grid1), dim3(256), 0, stream, g1);
   if (!launched_ok(FM_KERNEL_GATEUP)) return FM_EHIP;
   if (!mark(FM_KERNEL_DOWN, 0)) return FM_EHIP;
-  if (pl.large)
+  if (pl.big)
+    hipLaunchKernelGGL(fm_gemm_big_kernel<false>, dim3(grid2), dim3(512), 0, stream, g2);
+  else if (pl.large)
     hipLaunchKernelGGL(fm_gemm_kernel<false>, dim3(grid2), dim3(256), 0, stream, g2);
   else if (streamed && pl.pb == 1)
     hipLaunchKernelGGL((fm_stream_kernel<false, 1>), dim3(grid2), dim3(256), 0, stream, g2);

@@ -18,12 +18,13 @@ from __future__ import annotations
 
 import torch
 
-__all__ = ["fused_moe", "FLAG_LARGE_TILES", "FLAG_SMALL_TILES"]
+__all__ = ["fused_moe", "FLAG_LARGE_TILES", "FLAG_SMALL_TILES", "FLAG_BIG_TILES"]
 
 # Tile choice (fm_args.flags in include/fused_moe.h); 0 lets the library
 # choose from the tokens per expert.
 FLAG_LARGE_TILES = 1
 FLAG_SMALL_TILES = 2
+FLAG_BIG_TILES = 4
 
 _op = None  # the extension's fused_moe once it is loaded
 

@@ -167,7 +167,7 @@ def hc_make_args(mixes, scale, base, pre, post, comb, iters=20, eps=1e-6, flags=
 # ---------------------------------------------------------------------------
 FM_LIB_PATH = os.path.join(_HERE, "lib", "libfused_moe_gfx950.so")
 FM_OK, FM_EINVAL, FM_EUNSUPPORTED, FM_EWORKSPACE, FM_EHIP = range(5)
-FM_FLAG_LARGE_TILES, FM_FLAG_SMALL_TILES = 1, 2
+FM_FLAG_LARGE_TILES, FM_FLAG_SMALL_TILES, FM_FLAG_BIG_TILES = 1, 2, 4
 FM_KERNELS = ("route", "plan", "gateup", "down", "reduce")  # FM_KERNEL_* order
 FM_KERNEL_COUNT = len(FM_KERNELS)
 

@@ -109,11 +109,11 @@ def test_renormalize(gpu_sa, shape):
     assert (ref.double() - plain.double()).abs().max() > 1e-2  # the flag matters here
 
 
-@pytest.mark.parametrize("flags", [1, 2], ids=["large", "small"])
+@pytest.mark.parametrize("flags", [1, 2, 4], ids=["large", "small", "big"])
 @pytest.mark.parametrize("shape", [(64, 2048, 1024, 8, 2), (512, 1024, 512, 64, 6),
                                    (200, 256, 128, 4, 2)])
 def test_forced_tiles(gpu_sa, shape, flags):
-    """Both GEMM kernels on the same inputs, whichever the library would pick."""
+    """Every GEMM kernel on the same inputs, whichever the library would pick."""
     M, K, N, E, topk = shape
     hidden, w1, w2, score = make_inputs(M, K, N, E, seed=4)
     out = op(hidden, w1, w2, score, topk, flags=flags)
@@ -137,8 +137,22 @@ def test_every_token_on_one_expert(gpu_sa):
     hidden, w1, w2, score = make_inputs(M, K, N, E, seed=7)
     score[:, 3] = 8.0
     ref = fused_moe_ref(*cpu(hidden, w1, w2, score), topk)
-    for flags in (0, 1, 2):
+    for flags in (0, 1, 2, 4):
         check(op(hidden, w1, w2, score, topk, flags=flags), ref, f"one expert, flags={flags}")
+
+
+@pytest.mark.parametrize("shape", [(1500, 512, 256, 8, 2), (700, 1024, 512, 4, 3),
+                                   (2048, 2048, 1024, 8, 2)])
+def test_big_tiles_equal_large_tiles(gpu_sa, shape):
+    """256-pair tiles (8 waves, 32-wide K stages) and 128-pair tiles (4 waves,
+    64-wide stages) run the same MFMA sequence per output element, so they
+    agree bit for bit, with full and ragged tiles, row blocks past the last
+    pair and pair halves without any."""
+    M, K, N, E, topk = shape
+    hidden, w1, w2, score = make_inputs(M, K, N, E, seed=9)
+    big = op(hidden, w1, w2, score, topk, flags=4)
+    large = op(hidden, w1, w2, score, topk, flags=1)
+    assert torch.equal(big, large)
 
 
 @pytest.mark.parametrize("shape", [(37, 256, 128, 4, 4), (5, 256, 128, 1, 1), (1, 256, 128, 256, 32),
@@ -193,7 +207,7 @@ def test_capi_matches_operator_and_times_kernels(gpu_sa, shape, flags):
     hidden, w1, w2, score = make_inputs(M, K, N, E, seed=10)
     ref = op(hidden, w1, w2, score, topk, flags=flags)
     lib = sa_capi.fm_load()
-    assert lib.fm_abi_version() == 1
+    assert lib.fm_abi_version() == 2
     out = torch.full_like(hidden, float("nan"))
     a = sa_capi.fm_make_args(hidden, w1, w2, score, out, topk, flags=flags)
     n = sa_capi.fm_workspace_bytes(lib, a)
