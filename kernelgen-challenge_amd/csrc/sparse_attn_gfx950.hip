@@ -644,6 +644,10 @@ constexpr int kIdxScan = 4;   // LDS chunk reads per wave per batch
 
 __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexParams p) {
   extern __shared__ unsigned long long s_count[];  // [kv_len], byte q = count in query q
+  constexpr int kMaxChunks = int(sa::kMaxTileKv / 64);
+  __shared__ uint8_t s_cnz[kMaxChunks];    // 64-row chunk holds a named row
+  __shared__ int16_t s_clist[kMaxChunks];  // those chunks, ascending
+  __shared__ int s_nchunks;
   __shared__ int s_wtot[kIdxWaves];
   __shared__ int s_nvalid;   // valid slots of the tile
   __shared__ int s_bytes;    // sum of every count byte
@@ -659,7 +663,47 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   const int kvl = int(p.kv_len);
   const int topk = int(p.topk);
 
+  const int nchunks = (kvl + 63) / 64;
+  const int32_t* ib = p.idx + bi * p.si_b + q0 * p.si_m;
+  bool bad = false;  // an index outside [-1, kv_len)
+  int nvalid = 0;    // wave-uniform
+  auto count = [&](int v, int qq) {
+    const bool ok = v >= 0 && v < kvl;
+    if (ok) {
+      atomicAdd(&s_count[v], 1ull << (8 * qq));
+      s_cnz[v >> 6] = 1;
+    }
+    bad = bad || (!ok && v != -1);
+    nvalid += __popcll(__ballot(ok));
+  };
+  // vec4: topk, the row strides and the base are multiples of 4 int32
+  const int rv = topk / 4;  // int4 per query row
+  const int nv4 = qt * rv;
+  auto load4 = [&](int e0, int4 (&v)[kIdxVec], int (&qv)[kIdxVec]) {
+#pragma unroll
+    for (int u = 0; u < kIdxVec; ++u) {
+      const int e = e0 + u * kIdxThreads + tid;
+      const int qq = e / max(rv, 1);
+      qv[u] = qq;
+      v[u] = e < nv4 ? *reinterpret_cast<const int4*>(ib + qq * p.si_m + 4 * (e - qq * rv))
+                     : int4{-1, -1, -1, -1};
+    }
+  };
+  auto count4 = [&](const int4 (&v)[kIdxVec], const int (&qv)[kIdxVec]) {
+#pragma unroll
+    for (int u = 0; u < kIdxVec; ++u) {
+      count(v[u].x, qv[u]);
+      count(v[u].y, qv[u]);
+      count(v[u].z, qv[u]);
+      count(v[u].w, qv[u]);
+    }
+  };
+  // The first round of index loads flies while the count table is cleared.
+  int4 v0[kIdxVec];
+  int q0v[kIdxVec];
+  if (p.vec4) load4(0, v0, q0v);
   for (int i = tid; i < kvl; i += kIdxThreads) s_count[i] = 0ull;
+  for (int i = tid; i < nchunks; i += kIdxThreads) s_cnz[i] = 0;
   if (tid == 0) {
     s_first = kvl;
     s_nvalid = 0;
@@ -668,36 +712,13 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   __syncthreads();
 
   // ---- 1. count --------------------------------------------------------------
-  const int32_t* ib = p.idx + bi * p.si_b + q0 * p.si_m;
-  bool bad = false;  // an index outside [-1, kv_len)
-  int nvalid = 0;    // wave-uniform
-  auto count = [&](int v, int qq) {
-    const bool ok = v >= 0 && v < kvl;
-    if (ok) atomicAdd(&s_count[v], 1ull << (8 * qq));
-    bad = bad || (!ok && v != -1);
-    nvalid += __popcll(__ballot(ok));
-  };
-  if (p.vec4) {  // topk, the row strides and the base are multiples of 4 int32
-    const int rv = topk / 4;          // int4 per query row
-    const int nv = qt * rv;
-    for (int e0 = 0; e0 < nv; e0 += kIdxThreads * kIdxVec) {
+  if (p.vec4) {
+    count4(v0, q0v);
+    for (int e0 = kIdxThreads * kIdxVec; e0 < nv4; e0 += kIdxThreads * kIdxVec) {
       int4 v[kIdxVec];
       int qv[kIdxVec];
-#pragma unroll
-      for (int u = 0; u < kIdxVec; ++u) {
-        const int e = e0 + u * kIdxThreads + tid;
-        const int qq = e / max(rv, 1);
-        qv[u] = qq;
-        v[u] = e < nv ? *reinterpret_cast<const int4*>(ib + qq * p.si_m + 4 * (e - qq * rv))
-                      : int4{-1, -1, -1, -1};
-      }
-#pragma unroll
-      for (int u = 0; u < kIdxVec; ++u) {
-        count(v[u].x, qv[u]);
-        count(v[u].y, qv[u]);
-        count(v[u].z, qv[u]);
-        count(v[u].w, qv[u]);
-      }
+      load4(e0, v, qv);
+      count4(v, qv);
     }
   } else {
     const int nv = qt * topk;
@@ -720,24 +741,41 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   __syncthreads();
 
   // ---- 2. scan -----------------------------------------------------------------
-  const int nchunks = (kvl + 63) / 64;
-  const int cpw = (nchunks + kIdxWaves - 1) / kIdxWaves;
-  const int c_lo = min(nchunks, wave * cpw);
-  const int c_hi = min(nchunks, c_lo + cpw);
+  // Only the 64-row chunks holding a named row are scanned (a high-locality
+  // tile names a few dozen of 256): wave 0 lists them in ascending order, and
+  // wave w takes the w-th contiguous eighth of that list, so the union stays
+  // in ascending row order across the waves.
+  if (wave == 0) {
+    int base = 0;
+    for (int c0 = 0; c0 < nchunks; c0 += 64) {
+      const bool nz = c0 + lane < nchunks && s_cnz[c0 + lane] != 0;
+      const unsigned long long bm = __ballot(nz);
+      if (nz) s_clist[base + __popcll(bm & ((1ull << lane) - 1ull))] = int16_t(c0 + lane);
+      base += __popcll(bm);
+    }
+    if (lane == 0) s_nchunks = base;
+  }
+  __syncthreads();
+  const int nlist = s_nchunks;
+  const int cpw = (nlist + kIdxWaves - 1) / kIdxWaves;
+  const int c_lo = min(nlist, wave * cpw);
+  const int c_hi = min(nlist, c_lo + cpw);
   int wcount = 0;  // wave-uniform
   int wfirst = kvl;
   int bytes = 0;   // this lane's sum of count bytes
   for (int c0 = c_lo; c0 < c_hi; c0 += kIdxScan) {
     unsigned long long wv[kIdxScan];
+    int ch[kIdxScan];
 #pragma unroll
     for (int u = 0; u < kIdxScan; ++u) {
-      const int i = (c0 + u) * 64 + lane;
+      ch[u] = c0 + u < c_hi ? int(s_clist[c0 + u]) : 0;
+      const int i = ch[u] * 64 + lane;
       wv[u] = (c0 + u < c_hi && i < kvl) ? s_count[i] : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < kIdxScan; ++u) {
       const unsigned long long bm = __ballot(wv[u] != 0ull);
-      if (bm != 0ull && wfirst == kvl) wfirst = (c0 + u) * 64 + __ffsll((long long)bm) - 1;
+      if (bm != 0ull && wfirst == kvl) wfirst = ch[u] * 64 + __ffsll((long long)bm) - 1;
       wcount += __popcll(bm);
       // the 8 bytes as four 16-bit pair sums, then their total
       const unsigned long long pairs =
@@ -778,15 +816,17 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   const unsigned long long below = (1ull << lane) - 1ull;  // lanes under this one
   for (int c0 = c_lo; c0 < c_hi; c0 += kIdxScan) {
     unsigned long long wv[kIdxScan];
+    int ch[kIdxScan];
 #pragma unroll
     for (int u = 0; u < kIdxScan; ++u) {
-      const int i = (c0 + u) * 64 + lane;
+      ch[u] = c0 + u < c_hi ? int(s_clist[c0 + u]) : 0;
+      const int i = ch[u] * 64 + lane;
       wv[u] = (c0 + u < c_hi && i < kvl) ? s_count[i] : 0ull;
     }
 #pragma unroll
     for (int u = 0; u < kIdxScan; ++u) {
       const unsigned long long bm = __ballot(wv[u] != 0ull);
-      if (wv[u] != 0ull) put(pos + __popcll(bm & below), (c0 + u) * 64 + lane, wv[u]);
+      if (wv[u] != 0ull) put(pos + __popcll(bm & below), ch[u] * 64 + lane, wv[u]);
       pos += __popcll(bm);
     }
   }
