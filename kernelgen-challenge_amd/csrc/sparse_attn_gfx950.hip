@@ -156,6 +156,11 @@ struct TileParams {
   int64_t sl_b, sl_m, sl_h;
   int64_t ntiles;
   FwdParams fwd;        // arguments of the queries run per query (nsplit = 1)
+  // Placed launch (no order kernel): work-group i runs tile xcd_tile(i), its
+  // step count and mode read from the index kernel's meta; a per-query tile's
+  // work-group runs that tile's queries itself.
+  int placed;
+  const int32_t* meta;
 };
 
 struct CombineParams {
@@ -1033,8 +1038,33 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  // one load: tile and step count (work-groups past the order are workers)
-  const int32_t entry = blockIdx.x < p.ntiles ? p.order[blockIdx.x] : 0;
+  int32_t entry;
+  if (p.placed) {
+    // At most one tile per CU and at least one per two, all starting at once:
+    // the order kernel's XCD-local placement, computed here (work-group i runs
+    // on XCD i % 8; XCD x takes the x-th eighth of the tiles in tile order).
+    const int n = int(p.ntiles);
+    const int x = int(blockIdx.x) % kXcds;
+    int first = 0;
+    for (int y = 0; y < x; ++y) first += (n - y + kXcds - 1) / kXcds;
+    const int t = first + int(blockIdx.x) / kXcds;
+    const int32_t* mt = p.meta + int64_t(t) * kMetaInts;
+    const int nU = __builtin_amdgcn_readfirstlane(mt[0]);
+    if (__builtin_amdgcn_readfirstlane(mt[1]) != kModeShared) {
+      const int64_t b0 = t / p.tiles_per_b;
+      const int64_t m0 = (t % p.tiles_per_b) * kTQ;
+      const int nq = int(min(int64_t(kTQ), p.m - m0));
+      for (int j = 0; j < nq; ++j) {
+        query_unit(p.fwd, b0 * p.m + m0 + j, sm.q);
+        __syncthreads();
+      }
+      return;
+    }
+    entry = int32_t(((1 + (nU + kTileRows - 1) / kTileRows) << kOrderTileBits) | t);
+  } else {
+    // one load: tile and step count (work-groups past the order are workers)
+    entry = blockIdx.x < p.ntiles ? p.order[blockIdx.x] : 0;
+  }
   if ((entry >> kOrderTileBits) == 0) {
     // Per-query worker: the work-groups from the first per-query tile's
     // order entry to the end of the grid stride over the work list.
@@ -1721,6 +1751,13 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
                a->sidx[0] % 4 == 0 && a->sidx[1] % 4 == 0) ? 1 : 0;
     int32_t* order = reinterpret_cast<int32_t*>(ws + plan.order_off);
     int32_t* pq = reinterpret_cast<int32_t*>(ws + plan.pq_off);
+    // Between half as many tiles as CUs and as many, every tile starts at
+    // once and the order kernel's placement is a formula: the tile kernel
+    // applies it itself and that launch is skipped. (Fewer tiles keep the
+    // order kernel, whose per-query work list spreads the queries of
+    // per-query tiles over every CU. An index plan always holds an order.)
+    const bool placed = (a->flags & SA_FLAG_PLANNED) == 0 && what == Launch::kCall &&
+                        2 * plan.ntiles >= cus && plan.ntiles <= cus;
     if ((a->flags & SA_FLAG_PLANNED) == 0 || what == Launch::kPlanOnly) {
       const size_t lds = size_t(a->kv_len) * sizeof(unsigned long long);
       if (lds > 65536 &&
@@ -1732,6 +1769,8 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
                          lds, stream, ip);
       if (hipGetLastError() != hipSuccess) return SA_EHIP;
       if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
+    }
+    if (!placed && ((a->flags & SA_FLAG_PLANNED) == 0 || what == Launch::kPlanOnly)) {
       if (!mark(SA_KERNEL_ORDER, 0)) return SA_EHIP;
       OrderParams op{};
       op.meta = ip.meta;
@@ -1774,12 +1813,15 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.sl_h = a->slse[2];
     tp.ntiles = plan.ntiles;
     tp.fwd = p;
-    // One work-group per tile, then one per compute unit more: the queries of
-    // per-query tiles are run by the work-groups of those tiles' order
-    // entries and these (an empty work list costs them one read each).
+    tp.placed = placed ? 1 : 0;
+    tp.meta = ip.meta;
+    // Ordered: one work-group per tile, then one per compute unit more: the
+    // queries of per-query tiles are run by the work-groups of those tiles'
+    // order entries and these (an empty work list costs them one read each).
+    // Placed: one work-group per tile.
+    const int64_t grid = placed ? plan.ntiles : plan.ntiles + cus;
     if (!mark(SA_KERNEL_TILE, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles + cus)), dim3(kThreads), 0,
-                       stream, tp);
+    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(grid)), dim3(kThreads), 0, stream, tp);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
     if (!mark(SA_KERNEL_TILE, 1)) return SA_EHIP;
     return SA_OK;

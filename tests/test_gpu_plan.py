@@ -143,3 +143,58 @@ def test_capi_planned_launches(gpu_sa, shape, plain, planned):
     assert sa_capi.forward_events(lib, a, stream, none) == planned
     torch.cuda.synchronize()
     assert torch.equal(o, ref)
+
+
+def placed_cases():
+    """Shapes whose tiles number between half the CUs and the CUs: the plain
+    call places them itself (no order kernel)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    m = 8 * cus  # cus tiles
+    return {
+        "high locality": lambda: (*[x.to(DEV) for x in wl.make_config_inputs("high_locality")[:4]],
+                                  wl.SCALE),
+        "windows, ragged": lambda: windows(1, m - 5, 3000, seed=12),
+        "per-query tiles": lambda: case(1, m // 2 + 8, 16384, 256, seed=13, minus1=0.1),
+        "mixed, bad index": lambda: case(2, m // 2, 700, 128, seed=14, minus1=0.3),
+    }
+
+
+@pytest.mark.parametrize("name", ["high locality", "windows, ragged", "per-query tiles",
+                                  "mixed, bad index"])
+def test_placed_tiles_match_ordered(gpu_sa, name):
+    """A plain call that places its tiles itself equals the planned call,
+    whose tiles run in the order kernel's placement, bit for bit (o, lse and
+    the error word), and it skips the order kernel."""
+    q, kv, sink, idx, sc = placed_cases()[name]()
+    if name == "mixed, bad index":
+        idx[1, 17, 3] = kv.shape[1] + 5
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    lib = sa_capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for planned in (False, True):
+        o = torch.full_like(q, float("nan"))
+        lse = torch.full(q.shape[:3], float("nan"), device=DEV)
+        err = torch.zeros(1, dtype=torch.int32, device=DEV)
+        a = sa_capi.make_args(q, kv, sink, idx, o, sc, err=err, lse=lse)
+        n = sa_capi.workspace_bytes(lib, a)
+        ws = torch.full((max(n, 1),), 0xAB, dtype=torch.uint8, device=DEV)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), n
+        if planned:
+            sa_capi.check(lib, lib.sa_plan_indices(ctypes.byref(a), ctypes.c_void_p(stream)),
+                          "plan")
+            a.flags = sa_capi.SA_FLAG_PLANNED
+        none = [None] * (2 * sa_capi.SA_KERNEL_COUNT)
+        launched = sa_capi.forward_events(lib, a, stream, none)
+        torch.cuda.synchronize()
+        outs.append((o, lse, int(err.item()), launched))
+    (o1, l1, e1, k1), (o2, l2, e2, k2) = outs
+    expect_plan(q, kv, idx, tiles=True)
+    ntiles = q.shape[0] * -(-q.shape[1] // 8)
+    assert 2 * ntiles >= cus and ntiles <= cus, "the shape must be in the placed regime"
+    assert k1 == INDEX | TILE and k2 == TILE
+    assert torch.equal(o1, o2) and torch.equal(l1, l2)
+    assert e1 == e2 == (1 if name == "mixed, bad index" else 0)
+    if name == "high locality":  # and the values themselves, on a sample
+        sampled_check(o1, q.cpu(), kv.cpu(), sink.cpu(), idx.cpu(), sc,
+                      [(0, 0), (1, 129), (2, 300), (3, 511)], "placed high locality")
