@@ -410,9 +410,23 @@ MOE_WORKLOADS = [  # track-03/workloads.py:3-12: label, M, K, N, E, topk
     ("prefill", 512, 2048, 1024, 64, 6), ("prefill", 4096, 2048, 1024, 64, 6),
 ]
 MOE_KERNEL_NAMES = {"route": "fm_route_kernel", "plan": "fm_plan_kernel",
-                    "gateup": "fm_gemm_kernel<true> / fm_skinny_kernel<true>",
-                    "down": "fm_gemm_kernel<false> / fm_skinny_kernel<false>",
                     "reduce": "fm_reduce_kernel"}
+
+
+def moe_gemm_kernel(M, N, E, topk, gated):
+    """The GEMM kernel fused_moe launches for this shape with flags 0: the
+    tile choice of make_plan in csrc/fused_moe_gfx950.hip, restated for the
+    report (the profiles' kernel traces name the launched kernel)."""
+    P = M * topk
+    avg = P / E
+    g = "true" if gated else "false"
+    if avg > 24.0:
+        big = avg >= 256.0 and (P // 256) * (N // 128) >= 256
+        return f"fm_gemm_big_kernel<{g}>" if big else f"fm_gemm_kernel<{g}>"
+    pb = 4 if avg > 24.0 and N % 256 == 0 else 2 if avg > 12.0 else 1
+    if N % 256 == 0:
+        return f"fm_stream_kernel<{g}, {pb}>"
+    return f"fm_skinny_kernel<{g}, {pb}>"
 
 
 def moe_inputs(M, K, N, E, seed):
@@ -527,10 +541,11 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
             if dom == "gateup" else None
         if tr:
             roof.update({"traffic_commit": tr[1], "traffic_profile": tr[2]})
-        roof.update({"traffic": tr[0] if tr else None, "kernel": MOE_KERNEL_NAMES[dom],
+        names = dict(MOE_KERNEL_NAMES, gateup=moe_gemm_kernel(M, N, E, topk, True),
+                     down=moe_gemm_kernel(M, N, E, topk, False))
+        roof.update({"traffic": tr[0] if tr else None, "kernel": names[dom],
                      "kernel_us": round(times[dom] * 1e3, 2),
-                     "kernel_us_all": {MOE_KERNEL_NAMES[k]: round(v * 1e3, 2)
-                                       for k, v in times.items()}})
+                     "kernel_us_all": {names[k]: round(v * 1e3, 2) for k, v in times.items()}})
         rec = {"metric": "fused_moe µs/call, TFLOP/s + HBM GB/s (% roofline)",
                "value": round(flops / t / 1e12, 3), "unit": "TFLOP/s", "n_gpus": 1,
                "steps": steps, "warmup": warmup, "us_per_call": round(ms * 1e3, 2),
