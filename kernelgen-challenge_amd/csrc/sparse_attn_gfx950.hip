@@ -82,12 +82,21 @@ constexpr float kRescaleLog2 = 8.f;
 constexpr float kTileMaxJump = 24.f;
 
 constexpr int kTQ = sa::kTileQueries;       // queries per shared tile
-// A tile is shared when the dense (query x union row) MFMA work is at most
-// this multiple of its valid (query, slot) pairs. Measured on MI355X, the
-// shared-row kernel spends about 6.6 ns of one CU per dense (query, row) pair
-// and the per-query kernel, bound by the random row gather, about 37 ns per
-// valid pair: the per-query path pays off only above a waste of about 5.
-constexpr int kSharedWaste = 4;
+// A tile is shared when the shared-row kernel's CU time for it is below the
+// per-query kernel's for its queries, with a margin for the per-query side.
+// Measured on MI355X (CU time, nanoseconds): a shared tile costs about
+// 10 000 (start and epilogue) plus 6.6 per dense (tile query x union row)
+// pair, all 8 columns counted whatever the tile holds; a per-query unit costs
+// about 4 900 (index compaction, first gathers, epilogue) plus 35 per valid
+// slot (the random row gather). Fitted to causal prefill and long context,
+// and checked on the contest prefill shapes: at topk 128 the tiles the old
+// rule (dense work at most 4x the valid slots) sent per query run 12-33 %
+// faster shared.
+constexpr int64_t kSharedTileNs = 10000;
+constexpr int64_t kSharedPairNs10 = 66;   // x 10
+constexpr int64_t kQueryUnitNs = 4900;
+constexpr int64_t kQuerySlotNs = 35;
+constexpr int64_t kSharedMarginPct = 85;  // shared only below 85 % of per-query
 
 static_assert(kListCap % kThreads == 0, "compaction split");
 static_assert(kRowsPerWave == 16, "one 16-row MFMA block per wave");
@@ -841,10 +850,11 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   if (tid == 0) {
     const int total = s_nvalid;
     const bool overflow = s_bytes != total;  // a count carried
-    // shared when the dense (query x union row) work is at most
-    // kSharedWaste times the valid slots
-    const bool shared =
-        !overflow && (p.force != 0 || int64_t(qt) * nU <= kSharedWaste * int64_t(total));
+    // shared when that is cheaper (see kSharedTileNs)
+    const int64_t shared_ns10 = 10 * kSharedTileNs + kSharedPairNs10 * kTQ * int64_t(nU);
+    const int64_t query_ns10 = 10 * (kQueryUnitNs * qt + kQuerySlotNs * int64_t(total));
+    const bool cheaper = 100 * shared_ns10 <= kSharedMarginPct * query_ns10;
+    const bool shared = !overflow && (p.force != 0 || cheaper);
     int32_t* meta = p.meta + tile * kMetaInts;
     meta[0] = nU;
     meta[1] = shared ? kModeShared : sa::kModePerQuery;
