@@ -411,6 +411,7 @@ MOE_WORKLOADS = [  # track-03/workloads.py:3-12: label, M, K, N, E, topk
 ]
 MOE_KERNEL_NAMES = {"route": "fm_route_kernel", "plan": "fm_plan_kernel",
                     "reduce": "fm_reduce_kernel"}
+MOE_FUSED_ROUTE_TOKENS = 16  # kFusedRouteTokens in csrc/fused_moe_gfx950.hip
 
 
 def moe_gemm_kernel(M, N, E, topk, gated):
@@ -543,6 +544,9 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
             roof.update({"traffic_commit": tr[1], "traffic_profile": tr[2]})
         names = dict(MOE_KERNEL_NAMES, gateup=moe_gemm_kernel(M, N, E, topk, True),
                      down=moe_gemm_kernel(M, N, E, topk, False))
+        if M <= MOE_FUSED_ROUTE_TOKENS:  # routing and plan in one launch
+            times.pop("route", None)
+            names["plan"] = "fm_route_plan_kernel"
         roof.update({"traffic": tr[0] if tr else None, "kernel": names[dom],
                      "kernel_us": round(times[dom] * 1e3, 2),
                      "kernel_us_all": {names[k]: round(v * 1e3, 2) for k, v in times.items()}})

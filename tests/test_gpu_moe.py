@@ -201,7 +201,8 @@ def test_bad_inputs_raise(gpu_sa):
 
 
 @pytest.mark.parametrize("shape,flags", [((64, 2048, 1024, 8, 2), 0),
-                                         ((600, 512, 256, 8, 2), 0)])
+                                         ((600, 512, 256, 8, 2), 0),
+                                         ((5, 512, 256, 64, 6), 0)])
 def test_capi_matches_operator_and_times_kernels(gpu_sa, shape, flags):
     M, K, N, E, topk = shape
     hidden, w1, w2, score = make_inputs(M, K, N, E, seed=10)
@@ -220,10 +221,14 @@ def test_capi_matches_operator_and_times_kernels(gpu_sa, shape, flags):
     torch.cuda.synchronize()
     mask = sa_capi.fm_forward_events(lib, a, stream.cuda_stream, evs)
     torch.cuda.synchronize()
-    assert mask == (1 << sa_capi.FM_KERNEL_COUNT) - 1
+    every = (1 << sa_capi.FM_KERNEL_COUNT) - 1
+    # up to 16 tokens, routing and plan are one launch (reported as the plan)
+    route = 1 << sa_capi.FM_KERNELS.index("route")
+    assert mask == (every & ~route if M <= 16 else every)
     assert torch.equal(out, ref)
     for k in range(sa_capi.FM_KERNEL_COUNT):
-        assert evs[2 * k].elapsed_time(evs[2 * k + 1]) > 0.0
+        if (mask >> k) & 1:
+            assert evs[2 * k].elapsed_time(evs[2 * k + 1]) > 0.0
     # a workspace one byte short is refused before any device work
     a.workspace_bytes = n - 1
     out.fill_(float("nan"))
