@@ -329,25 +329,31 @@ __device__ __forceinline__ float wave_sum16(float x) {
 // ============================================================================
 // per-query kernel
 // ============================================================================
-// The rows of a part stream through a ring of kQRing LDS buffers of kQRows
+// The rows of a part stream through a ring of kRing LDS buffers of kQRows
 // rows each, filled by LDS-DMA (one 1 KiB row per wave instruction). While
-// the work-group computes on one buffer, the gathers of the next kQAhead
-// steps are in flight (96 KiB per work-group), so a short part (decode) has
-// its whole gather issued within its first steps, and a long one keeps
-// enough bytes in flight per CU to run at the random-row gather rate.
+// the work-group computes on one buffer, the gathers of the next kRing - 1
+// steps are in flight.
+//  * kRing = 4 (96 KiB in flight per work-group, 145 KiB of LDS: one
+//    work-group per CU): a short part (decode) has its whole gather issued
+//    within its first steps, and a long one keeps enough bytes in flight per
+//    CU to run at the random-row gather rate.
+//  * kRing = 2 (77 KiB of LDS: two work-groups per CU), for launches with
+//    several work-groups per CU: one work-group's start (index load,
+//    compaction, first gathers) and end overlap the other's gathers.
 constexpr int kQRows = 32;
-constexpr int kQRing = 4;
-constexpr int kQAhead = kQRing - 1;
 constexpr int kQRowsPerWave = kQRows / kWaves;  // rows of a step each wave gathers
-static_assert(kQAhead == 3 && kQRowsPerWave == 8, "the vmcnt waits of the ring");
+static_assert(kQRowsPerWave == 8, "the vmcnt waits of the ring");
 
-struct QuerySmem {
-  uint8_t tile[kQRing][kQRows * kRowStride];
+template <int kRing>
+struct QuerySmemT {
+  uint8_t tile[kRing][kQRows * kRowStride];
   int32_t list[kListCap];
   __bf16 p[kHeads * kQRows];
   float red[kWaves][kHeads];
   int cnt[kWaves];
 };
+using QuerySmem = QuerySmemT<4>;
+static_assert(sizeof(QuerySmemT<2>) <= 80 * 1024, "two ring-2 work-groups per CU");
 
 // Waits until at most the gathers of `later` (0..2) steps issued after the
 // current one are outstanding: this wave's rows of the current step are in
@@ -364,8 +370,12 @@ __device__ __forceinline__ void wait_ring(int later) {
 // One (query, topk part) unit of the per-query kernel. Leaves every wave past
 // its last LDS access of `sm` only after the work-group's final barrier, so a
 // following unit may reuse `sm` after one more __syncthreads().
+template <int kRing>
 __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t unit,
-                                           QuerySmem& sm) {
+                                           QuerySmemT<kRing>& sm) {
+  constexpr int kQRing = kRing;
+  constexpr int kQAhead = kRing - 1;
+  static_assert(kQAhead >= 1 && kQAhead <= 3, "wait_ring covers up to 2 later steps");
   auto& s_list = sm.list;
   auto& s_p = sm.p;
   auto& s_red = sm.red;
@@ -619,9 +629,11 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
 }
 
 // Work-group i runs unit i (query i / nsplit, part i % nsplit).
-__global__ void __launch_bounds__(kThreads, 1) sa_fwd_query_kernel(const FwdParams p) {
-  __shared__ __attribute__((aligned(16))) QuerySmem sm;
-  query_unit(p, blockIdx.x, sm);
+template <int kRing>
+__global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
+    sa_fwd_query_kernel(const FwdParams p) {
+  __shared__ __attribute__((aligned(16))) QuerySmemT<kRing> sm;
+  query_unit<kRing>(p, blockIdx.x, sm);
 }
 
 // ============================================================================
@@ -1065,7 +1077,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       const int64_t m0 = (t % p.tiles_per_b) * kTQ;
       const int nq = int(min(int64_t(kTQ), p.m - m0));
       for (int j = 0; j < nq; ++j) {
-        query_unit(p.fwd, b0 * p.m + m0 + j, sm.q);
+        query_unit<4>(p.fwd, b0 * p.m + m0 + j, sm.q);
         __syncthreads();
       }
       return;
@@ -1082,7 +1094,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     const int nshared = __builtin_amdgcn_readfirstlane(p.pq[1]);
     const int workers = int(gridDim.x) - nshared;
     for (int k = int(blockIdx.x) - nshared; k < nq; k += workers) {
-      query_unit(p.fwd, p.pq[2 + k], sm.q);
+      query_unit<4>(p.fwd, p.pq[2 + k], sm.q);
       __syncthreads();  // every wave is done with the LDS before the next unit
     }
     return;
@@ -1364,7 +1376,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       // The tile's queries run per query here (online rescale); nothing of
       // the tile was written and no transfer is in flight.
       for (int j = 0; j < qt; ++j) {
-        query_unit(p.fwd, bi * p.m + q0 + j, sm.q);
+        query_unit<4>(p.fwd, bi * p.m + q0 + j, sm.q);
         __syncthreads();
       }
       return;
@@ -1839,7 +1851,13 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
   if (what == Launch::kPlanOnly) return SA_OK;  // per-query plans keep no index state
 
   if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
-  hipLaunchKernelGGL(sa_fwd_query_kernel, dim3(unsigned(p.nblocks)), dim3(kThreads), 0, stream, p);
+  // two work-groups per CU once there are at least two per CU to run
+  if (p.nblocks >= 2 * int64_t(cus))
+    hipLaunchKernelGGL(sa_fwd_query_kernel<2>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
+                       stream, p);
+  else
+    hipLaunchKernelGGL(sa_fwd_query_kernel<4>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
+                       stream, p);
   if (hipGetLastError() != hipSuccess) return SA_EHIP;
   if (!mark(SA_KERNEL_QUERY, 1)) return SA_EHIP;
   if (plan.nsplit > 1) {
