@@ -155,7 +155,11 @@ def time_calls(fn, sets, scale, steps, warmup, plans=None):
 
 def kernel_times(sets, scale, steps, warmup):
     """Average launch duration (ms) of each kernel over `steps` calls, from
-    the HIP events sa_forward_events records on the calls' stream."""
+    the HIP events sa_forward_events records on the calls' stream, and each
+    kernel's share of the valid slots. In a shared-row plan the tile kernel
+    runs the shared tiles' slots and the per-query kernel the others: the
+    tile meta the index kernel leaves at workspace offset 0 (per tile: union
+    size, mode, valid slots, overflow) tells them apart."""
     import sa_capi
     lib = sa_capi.load()
     stream = torch.cuda.current_stream()
@@ -183,7 +187,16 @@ def kernel_times(sets, scale, steps, warmup):
              if (masks[i] >> k) & 1]
         if d:
             times[name] = sum(d) / len(d)
-    return times
+    shares = {"query": 1.0, "combine": 1.0}
+    if masks[-1] & (1 << sa_capi.KERNELS.index("index")):
+        b, m = sets[0][0].shape[:2]
+        ntiles = b * -(-m // 8)
+        meta = ws[:16 * ntiles].view(torch.int32).view(ntiles, 4).cpu().long()
+        total = int(meta[:, 2].sum())
+        shared = int(meta[meta[:, 1] == 1, 2].sum())
+        shares = {"tile": shared / total if total else 1.0,
+                  "query": (total - shared) / total if total else 0.0}
+    return times, shares
 
 
 def cpu_baseline(cpu_inputs, target_s=4.0, runs=3):
@@ -225,14 +238,13 @@ def cpu_baseline(cpu_inputs, target_s=4.0, runs=3):
             "us_per_call_extrapolated": round(dt / nq * b * m * 1e6, 1)}
 
 
-def roofline(name, flops, compulsory, times):
-    """The dominant kernel's algorithmic rate. A call launches either the
-    shared-row kernel (which also runs the queries of per-query tiles) or the
-    per-query kernel, so the dominant one processes every valid slot."""
+def roofline(name, flops, compulsory, times, shares):
+    """The dominant kernel's algorithmic rate: its share of the call's flops
+    (or compulsory bytes) over its launch duration."""
     dom = max(times, key=times.get)
     t = times[dom] * 1e-3
     mfma_bound = flops / (PEAK_MFMA_TFLOPS * 1e12) >= compulsory / (PEAK_HBM_GBPS * 1e9)
-    share = 1.0 if dom in ("tile", "query", "combine") else 0.0
+    share = shares.get(dom, 0.0)
     if mfma_bound:
         ach = flops * share / t / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_MFMA_TFLOPS,
@@ -264,7 +276,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     n_valid, flops, gathered, uniq, compulsory = algorithmic(idx, b, m)
     settle_calls = settle(submission.sparse_attn, sets, scale, settle_s)
     ms = time_calls(submission.sparse_attn, sets, scale, steps, warmup)
-    times = kernel_times(sets, scale, steps, warmup)
+    times, shares = kernel_times(sets, scale, steps, warmup)
     # the same calls with each input set's index plan made beforehand
     # (sparse_attn_plan): what a call costs when its indices are reused
     plans = [submission.sparse_attn_plan(s[0], s[1], s[3]) for s in sets]
@@ -296,7 +308,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                    "n_valid": n_valid, "unique_rows": uniq,
                    "flops_alg": flops, "gathered_bytes": gathered,
                    "compulsory_bytes": compulsory, "input_sets_rotated": nsets},
-        "roofline": roofline(name, flops, compulsory, times),
+        "roofline": roofline(name, flops, compulsory, times, shares),
         "planned": {"us_per_call": round(ms_planned * 1e3, 2),
                     "value": round(flops / (ms_planned * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
                     "note": "index plan made before the timed calls and reused"},

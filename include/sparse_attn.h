@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 4
+#define SA_ABI_VERSION 5
 
 /* Return codes. */
 enum {
@@ -198,12 +198,20 @@ int sa_plan_indices(const sa_args* a, void* hip_stream);
 #define SA_NOALLOC_SCRATCH_BYTES (48u << 20)
 int sa_forward_noalloc(const sa_args* a, void* hip_stream);
 
-/* Kernels of one sa_forward call, in launch order. */
+/*
+ * Kernels of one sa_forward call. Launch order: per-query plans QUERY, then
+ * COMBINE when split; shared-row (tile) plans INDEX (unless SA_FLAG_PLANNED),
+ * QUERY, TILE. In a tile plan the QUERY launch runs the queries of the tiles
+ * the index kernel made per query, and makes the longest-first tile order
+ * in its first work-group. (Version 5: the order no longer has a launch of
+ * its own, so bit SA_KERNEL_ORDER is never set.)
+ */
 enum {
   SA_KERNEL_INDEX = 0,    /* row unions of shared-row tiles (tile plans)   */
-  SA_KERNEL_ORDER = 1,    /* longest-first tile order (tile plans)         */
+  SA_KERNEL_ORDER = 1,    /* not launched since version 5                  */
   SA_KERNEL_TILE = 2,     /* shared-row tiles (tile plans)                 */
-  SA_KERNEL_QUERY = 3,    /* per-query parts (every plan)                  */
+  SA_KERNEL_QUERY = 3,    /* per-query parts; in tile plans the per-query
+                             tiles and the tile order                      */
   SA_KERNEL_COMBINE = 4,  /* merge of split-topk parts (split plans)       */
   SA_KERNEL_COUNT = 5
 };

@@ -21,8 +21,8 @@ int sa_host_plan(const sa_args* a, int num_cus, int64_t* nsplit, int64_t* split_
 }
 
 // out[0..6] = nsplit, split_len, tiles, tiles_per_b, ntiles, tile_cap, ws_bytes;
-// out[7..12] = workspace offsets of the tile meta, tile order, union rows,
-// multiplicities, per-query work list and split partials
+// out[7..11] = workspace offsets of the tile meta, tile order, union rows,
+// multiplicities and split partials
 int sa_host_plan_full(const sa_args* a, int num_cus, int64_t* out) {
   const int rc = sa::validate(a);
   if (rc != SA_OK) return rc;
@@ -38,8 +38,7 @@ int sa_host_plan_full(const sa_args* a, int num_cus, int64_t* out) {
   out[8] = int64_t(p.order_off);
   out[9] = int64_t(p.rows_off);
   out[10] = int64_t(p.cnts_off);
-  out[11] = int64_t(p.pq_off);
-  out[12] = int64_t(p.part_off);
+  out[11] = int64_t(p.part_off);
   return SA_OK;
 }
 

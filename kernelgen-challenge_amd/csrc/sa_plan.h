@@ -36,8 +36,8 @@ constexpr int kMetaInts = 4;  // per tile: union size, mode, valid slots, spare
 //  * shared-row path (`tiles`): an index kernel builds each tile's row union,
 //    a one-work-group pass orders the tiles by descending step count (longest
 //    first, so the last work-groups to start are the short ones), then tiles
-//    whose queries overlap enough run in the shared-row kernel and the rest
-//    per query, by that kernel's remaining work-groups.
+//    whose queries overlap enough run in the shared-row kernel, and the
+//    queries of the others in a per-query launch after it.
 struct Plan {
   int64_t units;       // b * m
   int nsplit;          // parts per query (1 = no combine pass)
@@ -48,7 +48,7 @@ struct Plan {
   int64_t tile_cap;    // union entries stored per tile (multiple of kTileRows);
                        // each has a 32-bit row offset and kTileQueries fp16
                        // log2 multiplicities
-  size_t meta_off, order_off, rows_off, cnts_off, pq_off, part_off;  // workspace byte offsets
+  size_t meta_off, order_off, rows_off, cnts_off, part_off;  // workspace byte offsets
   size_t ws_bytes;     // total workspace
 };
 
@@ -180,8 +180,6 @@ inline Plan make_plan(const sa_args* a, int num_cus) {
     off = round_up(off + size_t(p.ntiles) * p.tile_cap * 4, 256);
     p.cnts_off = off;  // fp16 log2 multiplicity per (union entry, tile query)
     off = round_up(off + size_t(p.ntiles) * p.tile_cap * kTileQueries * 2, 256);
-    p.pq_off = off;    // per-query work list: count, shared tiles, then up to b * m query ids
-    off = round_up(off + size_t(2 + p.units) * 4, 256);
   }
   if (p.nsplit > 1) {
     p.part_off = off;

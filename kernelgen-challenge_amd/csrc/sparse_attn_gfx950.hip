@@ -18,22 +18,23 @@
 //   batch: counts every valid index of the tile's queries in an LDS table
 //   (one byte per query), writes the row union in ascending order (32-bit
 //   byte offsets) with an fp16 log2 multiplicity per (query, row), and marks
-//   the tile "shared" when the dense (query x union row) work is at most 4x
-//   its valid slots, else "per query".
-// sa_tile_order_kernel  one work-group: counting sort of the tiles by
-//   descending step count, so the longest tiles are launched first.
+//   the tile "shared" when the shared-row kernel would spend less CU time on
+//   it than the per-query kernel on its queries, else "per query".
 // sa_fwd_tile_kernel  one work-group per shared tile (128 query-head
 //   columns): gathers each union row once (LDS-DMA, 1 KiB per instruction),
 //   S^T = K . Q^T with each wave owning two queries, P through LDS, O += P . V
 //   with each wave owning a quarter of d; v_mfma_f32_32x32x16_bf16; the
 //   softmax of one 32-row half runs between the MFMAs of the next. A fixed
 //   per-column reference replaces rescaling; a tile whose scores jump above
-//   it runs its queries per query in place. The work-groups past the shared
-//   tiles (and one per CU more) run the queries of per-query tiles.
-// sa_fwd_query_kernel  one work-group (4 wave64s) per (query, topk part):
-//   compacts the part's valid indices into LDS, then streams steps of 32
-//   gathered rows through a ring of 4 LDS buffers filled by LDS-DMA (three
-//   steps in flight). S^T = K . Q^T with v_mfma_f32_16x16x32_bf16 (wave w:
+//   it runs its queries per query in place.
+// sa_fwd_query_kernel  one work-group (4 wave64s) per (query, topk part);
+//   in a shared-row plan (before the shared-row kernel) one per tile, which
+//   runs the queries of a per-query tile in turn, and work-group 0 makes the
+//   tile order: a counting sort by descending step count, so the longest
+//   tiles are launched first. Compacts the part's valid indices into LDS,
+//   then streams steps of 32 gathered rows through a ring of LDS buffers
+//   filled by LDS-DMA (4 buffers, or 2 and two work-groups per CU when the
+//   launch has at least two per CU). S^T = K . Q^T with v_mfma_f32_16x16x32_bf16 (wave w:
 //   the step's rows 8w.., 16 heads, K = d = 512, Q^T resident in registers);
 //   online softmax with a per-head max across the waves through LDS;
 //   O += P . V with the same MFMA (wave w: d columns 128w..), its V operands
@@ -86,17 +87,42 @@ constexpr int kTQ = sa::kTileQueries;       // queries per shared tile
 // per-query kernel's for its queries, with a margin for the per-query side.
 // Measured on MI355X (CU time, nanoseconds): a shared tile costs about
 // 10 000 (start and epilogue) plus 6.6 per dense (tile query x union row)
-// pair, all 8 columns counted whatever the tile holds; a per-query unit costs
-// about 4 900 (index compaction, first gathers, epilogue) plus 35 per valid
-// slot (the random row gather). Fitted to causal prefill and long context,
-// and checked on the contest prefill shapes: at topk 128 the tiles the old
-// rule (dense work at most 4x the valid slots) sent per query run 12-33 %
-// faster shared.
+// pair, all 8 columns counted whatever the tile holds (causal prefill). The
+// queries of per-query tiles run in the per-query launch that follows the
+// shared-row kernel, two work-groups per CU, whose starts and ends overlap
+// each other's gathers: a query costs about 2 100 plus 27 per valid slot
+// (topk 128 at kv_len 1 024 - 16 384: 5.3-5.9 us per query; topk 640 at
+// kv_len 20 480: 19.2 us).
+// When every tile starts at once (between half as many tiles as CUs and as
+// many), the per-query launch's time adds to the slowest tile's instead of
+// filling in behind other tiles, and its work-groups have a CU each: a query
+// is priced at 4 900 plus 35 per slot. (At the lower price high locality's
+// longest tiles went per query and the call took 134 us instead of 116.)
 constexpr int64_t kSharedTileNs = 10000;
 constexpr int64_t kSharedPairNs10 = 66;   // x 10
-constexpr int64_t kQueryUnitNs = 4900;
-constexpr int64_t kQuerySlotNs = 35;
+constexpr int64_t kQueryUnitNs = 2100;
+constexpr int64_t kQuerySlotNs = 27;
+constexpr int64_t kPlacedQueryUnitNs = 4900;
+constexpr int64_t kPlacedQuerySlotNs = 35;
 constexpr int64_t kSharedMarginPct = 85;  // shared only below 85 % of per-query
+
+// The mode rule: shared when the tile's shared-row time is below
+// kSharedMarginPct % of its queries' per-query time.
+__host__ __device__ constexpr bool shared_is_cheaper(int64_t n_union, int64_t n_valid,
+                                                    int64_t queries, bool placed_regime) {
+  return 100 * (10 * kSharedTileNs + kSharedPairNs10 * kTQ * n_union) <=
+         kSharedMarginPct * 10 *
+             ((placed_regime ? kPlacedQueryUnitNs : kQueryUnitNs) * queries +
+              (placed_regime ? kPlacedQuerySlotNs : kQuerySlotNs) * n_valid);
+}
+
+// An order entry of the tile order kernel is (key << kOrderTileBits) | tile:
+// key 0 for a per-query tile, else 1 + its step count, so the shared-row
+// kernel learns its tile and step count from one load. A plan has at most
+// b * m / 4 <= 2^22 tiles.
+constexpr int kOrderTileBits = 22;
+static_assert(sa::kMaxUnits / (sa::kTileQueries / 2) <= (int64_t(1) << kOrderTileBits),
+              "tile ids fit the order entry");
 
 static_assert(kListCap % kThreads == 0, "compaction split");
 static_assert(kRowsPerWave == 16, "one 16-row MFMA block per wave");
@@ -109,6 +135,14 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4_t;
 typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+
+// Arguments of the tile order (see make_order).
+struct OrderParams {
+  const int32_t* meta;
+  int32_t* order;
+  int ntiles;
+  int cus;  // compute units of the device
+};
 
 struct FwdParams {
   const __bf16* q;
@@ -129,6 +163,11 @@ struct FwdParams {
   int nsplit;
   int64_t split_len;
   int64_t nblocks;      // grid size (units * nsplit)
+  // Shared-row plans (nsplit = 1): the index kernel's tile meta (the launch
+  // runs the queries of per-query tiles) and the tile order to make, if any.
+  const int32_t* meta;
+  int64_t tiles_per_b;
+  OrderParams ord;
 };
 
 struct IndexParams {
@@ -143,6 +182,7 @@ struct IndexParams {
   int64_t tiles_per_b, cap;
   int force;            // shared mode whenever the counts fit
   int vec4;             // indices readable as int4 (aligned base, strides and topk)
+  int placed_regime;    // every tile starts at once (see kPlacedQueryUnitNs)
 };
 
 struct TileParams {
@@ -150,10 +190,7 @@ struct TileParams {
   const __bf16* kv;
   const float* sink;
   __bf16* o;
-  // Per-query work list of the order kernel: pq[0] = number of queries,
-  // pq[1] = number of shared tiles, pq[2..] = flat query ids b * m + m_i.
-  const int32_t* pq;
-  const int32_t* order; // work-group i < ntiles runs entry order[i]
+  const int32_t* order; // work-group i runs entry order[i]
   const uint32_t* row_off;
   const _Float16* lcnt;
   int64_t m, cap, tiles_per_b;
@@ -164,10 +201,9 @@ struct TileParams {
   float* lse;           // fp32 [b, m, h] or null
   int64_t sl_b, sl_m, sl_h;
   int64_t ntiles;
-  FwdParams fwd;        // arguments of the queries run per query (nsplit = 1)
+  FwdParams fwd;        // arguments of the queries of aborted tiles (nsplit = 1)
   // Placed launch (no order kernel): work-group i runs tile xcd_tile(i), its
-  // step count and mode read from the index kernel's meta; a per-query tile's
-  // work-group runs that tile's queries itself.
+  // step count and mode read from the index kernel's meta.
   int placed;
   const int32_t* meta;
 };
@@ -511,7 +547,8 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
           for (int s = 0; s < 3; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 64 * s);
 #pragma unroll
           for (int s = 0; s < kDim / 32; ++s) {
-            if (s + 3 < kDim / 32) kf[(s + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (s + 3));
+            if (s + 3 < kDim / 32)
+              kf[(s + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (s + 3));
             sacc = mfma_16x16x32(kf[s & 3], qf[s], sacc);
             if constexpr (decltype(with_dma)::value) {
               if (s & 1) {
@@ -628,13 +665,6 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
   }
 }
 
-// Work-group i runs unit i (query i / nsplit, part i % nsplit).
-template <int kRing>
-__global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
-    sa_fwd_query_kernel(const FwdParams p) {
-  __shared__ __attribute__((aligned(16))) QuerySmemT<kRing> sm;
-  query_unit<kRing>(p, blockIdx.x, sm);
-}
 
 // ============================================================================
 // tile index kernel
@@ -676,6 +706,7 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   __shared__ int s_nchunks;
   __shared__ int s_wtot[kIdxWaves];
   __shared__ int s_nvalid;   // valid slots of the tile
+  __shared__ int s_nunion;   // rows named by the tile (first counts of a row)
   __shared__ int s_bytes;    // sum of every count byte
   __shared__ int s_first;
 
@@ -693,10 +724,11 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   const int32_t* ib = p.idx + bi * p.si_b + q0 * p.si_m;
   bool bad = false;  // an index outside [-1, kv_len)
   int nvalid = 0;    // wave-uniform
+  int nfresh = 0;    // this lane's counts that found their row's word at 0
   auto count = [&](int v, int qq) {
     const bool ok = v >= 0 && v < kvl;
     if (ok) {
-      atomicAdd(&s_count[v], 1ull << (8 * qq));
+      nfresh += atomicAdd(&s_count[v], 1ull << (8 * qq)) == 0ull ? 1 : 0;
       s_cnz[v >> 6] = 1;
     }
     bad = bad || (!ok && v != -1);
@@ -733,6 +765,7 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   if (tid == 0) {
     s_first = kvl;
     s_nvalid = 0;
+    s_nunion = 0;
     s_bytes = 0;
   }
   __syncthreads();
@@ -764,7 +797,24 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   }
   if (bad && p.err != nullptr) flag_bad_index(p.err);
   if (lane == 0 && nvalid != 0) atomicAdd(&s_nvalid, nvalid);
+  for (int off = 32; off > 0; off >>= 1) nfresh += __shfl_xor(nfresh, off);
+  if (lane == 0 && nfresh != 0) atomicAdd(&s_nunion, nfresh);
   __syncthreads();
+  // Each row's first count found its word at 0 (LDS atomics on one word are
+  // serialised), so s_nunion is the union size, and the mode can be decided
+  // now: a per-query tile needs no union, so its scan and write are skipped.
+  // (A count carry can only make a tile per query, below.)
+  const bool cheaper = shared_is_cheaper(s_nunion, s_nvalid, qt, p.placed_regime != 0);
+  if (p.force == 0 && !cheaper) {
+    if (tid == 0) {
+      int32_t* meta = p.meta + tile * kMetaInts;
+      meta[0] = s_nunion;
+      meta[1] = sa::kModePerQuery;
+      meta[2] = s_nvalid;
+      meta[3] = 0;
+    }
+    return;
+  }
 
   // ---- 2. scan -----------------------------------------------------------------
   // Only the 64-row chunks holding a named row are scanned (a high-locality
@@ -862,11 +912,7 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   if (tid == 0) {
     const int total = s_nvalid;
     const bool overflow = s_bytes != total;  // a count carried
-    // shared when that is cheaper (see kSharedTileNs)
-    const int64_t shared_ns10 = 10 * kSharedTileNs + kSharedPairNs10 * kTQ * int64_t(nU);
-    const int64_t query_ns10 = 10 * (kQueryUnitNs * qt + kQuerySlotNs * int64_t(total));
-    const bool cheaper = 100 * shared_ns10 <= kSharedMarginPct * query_ns10;
-    const bool shared = !overflow && (p.force != 0 || cheaper);
+    const bool shared = !overflow;  // and cheaper, or forced (above)
     int32_t* meta = p.meta + tile * kMetaInts;
     meta[0] = nU;
     meta[1] = shared ? kModeShared : sa::kModePerQuery;
@@ -876,123 +922,198 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
 }
 
 // ============================================================================
-// tile order kernel
+// tile order (the first work-group of the per-query launch)
 // ============================================================================
 // One work-group sorts the tiles by descending step count (a counting sort:
 // a shared tile's key is 1 + its step count, a per-query tile's 0). The
 // shared-row kernel's work-group i runs entry i; work-groups start in index
 // order, so the longest tiles start first and the short ones fill in at the
 // end. Tiles with equal keys may come in any order: each tile is independent.
-// The queries of per-query tiles go to the work list of the shared-row
-// kernel's per-query workers (pq[0] = count, pq[1] = number of shared tiles,
-// pq[2..] = flat query ids), in any order.
+// The per-query tiles' entries come last; the shared-row kernel's
+// work-groups of those entries return at once (the per-query launch runs
+// their queries).
 // When the shared tiles fit the first wave of the shared-row kernel's grid
 // (at most one per CU, so every one starts at once) their order cannot
 // change when they finish; they are then placed for L2 reuse instead. Work-
 // group i runs on XCD i % 8, and XCD x gets the x-th eighth of the shared
 // tiles in tile order: consecutive queries of one batch, whose row unions
 // overlap and which sweep their ascending unions in step, share that XCD's L2.
-constexpr int kOrderThreads = 1024;
 constexpr int kOrderKeys = int(sa::kMaxTileKv / kTileRows) + 2;
 constexpr int kOrderKeysPadded = (kOrderKeys + 63) / 64 * 64;
-// An order entry is (key << kOrderTileBits) | tile: key 0 for a per-query
-// tile, else 1 + its step count, so the shared-row kernel learns its tile and
-// step count from one load. A plan has at most b * m / 4 <= 2^22 tiles.
-constexpr int kOrderTileBits = 22;
-static_assert(sa::kMaxUnits / (sa::kTileQueries / 2) <= (int64_t(1) << kOrderTileBits),
-              "tile ids fit the order entry");
+constexpr int kOrderPer = 8;  // tiles per thread per pass (their loads issued together)
+// XCD placement handles at most this many tiles (every shared tile then
+// starts at once anyway)
+constexpr int kOrderPlaceMax = 1024;
+// tiles whose keys the first pass keeps in LDS for the second (16-bit keys)
+constexpr int kOrderKeyCache = 16384;
 static_assert(kOrderKeys <= (1 << (31 - kOrderTileBits)), "keys fit the order entry");
 
 constexpr int kXcds = 8;  // MI355X: work-groups are dealt to the 8 XCDs round-robin
 
-struct OrderParams {
-  const int32_t* meta;
-  int32_t* order;
-  int32_t* pq;
-  int ntiles;
-  int cus;  // compute units of the device
-  int64_t m, tiles_per_b;
+struct OrderSmem {
+  int pos[kOrderKeysPadded];
+  int wcount[kWaves];
+  uint16_t key[kOrderKeyCache];
 };
 
-__global__ void __launch_bounds__(kOrderThreads) sa_tile_order_kernel(const OrderParams p) {
-  __shared__ int s_pos[kOrderKeysPadded];
-  __shared__ int s_npq;
-  __shared__ int s_wshared[kOrderThreads / 64];
+// The tile order, made by one work-group of kThreads threads.
+__device__ void make_order(const OrderParams& p, OrderSmem& sm) {
   const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const unsigned long long below = (1ull << lane) - 1ull;
   const int32_t* meta = p.meta;
   const int ntiles = p.ntiles;
-  for (int i = tid; i < kOrderKeysPadded; i += kOrderThreads) s_pos[i] = 0;
-  if (tid == 0) s_npq = 0;
+  for (int i = tid; i < kOrderKeysPadded; i += kThreads) sm.pos[i] = 0;
   __syncthreads();
   auto key = [&](int t) {
     const int32_t* mt = meta + int64_t(t) * kMetaInts;
     return mt[1] == kModeShared ? (mt[0] + kTileRows - 1) / kTileRows + 1 : 0;
   };
-  for (int t = tid; t < ntiles; t += kOrderThreads) {
-    const int k = key(t);
-    atomicAdd(&s_pos[k], 1);
-    if (meta[int64_t(t) * kMetaInts + 1] != kModeShared) {
-      const int64_t bi = t / p.tiles_per_b;
-      const int64_t q0 = (t % p.tiles_per_b) * kTQ;
-      const int qt = int(min(int64_t(kTQ), p.m - q0));
-      const int pos = atomicAdd(&s_npq, qt);
-      for (int j = 0; j < qt; ++j) p.pq[2 + pos + j] = int32_t(bi * p.m + q0 + j);
+  const bool cached = ntiles <= kOrderKeyCache;
+  auto keys = [&](int t0, int (&k)[kOrderPer], bool from_lds) {
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u) {
+      const int t = t0 + u * kThreads + tid;
+      k[u] = t >= ntiles ? -1 : from_lds ? int(sm.key[t]) : key(t);
+    }
+  };
+  // Key 0 (every per-query tile) is counted per wave: one LDS atomic per wave
+  // instead of one per tile on a single word.
+  for (int t0 = 0; t0 < ntiles; t0 += kThreads * kOrderPer) {
+    int k[kOrderPer];
+    keys(t0, k, false);
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u) {
+      const unsigned long long z = __ballot(k[u] == 0);
+      if (k[u] > 0) atomicAdd(&sm.pos[k[u]], 1);
+      if (lane == 0 && z != 0ull) atomicAdd(&sm.pos[0], __popcll(z));
+      if (cached && k[u] >= 0) sm.key[t0 + u * kThreads + tid] = uint16_t(k[u]);
     }
   }
   __syncthreads();
-  const int nshared = ntiles - s_pos[0];  // shared tiles: every key above 0
-  if (tid == 0) {
-    p.pq[0] = s_npq;
-    p.pq[1] = nshared;
-  }
-  __syncthreads();  // every thread has read s_pos[0] before the scan rewrites it
-  if (nshared <= p.cus && ntiles <= kOrderThreads) {
+  const int nshared = ntiles - sm.pos[0];  // shared tiles: every key above 0
+  __syncthreads();  // every thread has read pos[0] before the scan rewrites it
+  static_assert(kOrderPlaceMax <= kThreads * kOrderPer && kOrderPlaceMax <= kOrderKeyCache,
+                "placement reads one pass of cached keys");
+  if (nshared <= p.cus && ntiles <= kOrderPlaceMax) {
     // Every shared tile starts at once: XCD-local placement (see above). A
     // tile's rank among the shared tiles in tile order picks its slot; the
     // per-query tiles' entries fill the slots after them.
-    const bool sh = tid < ntiles && key(tid) > 0;
-    const unsigned long long bm = __ballot(sh);
-    if ((tid & 63) == 0) s_wshared[tid >> 6] = __popcll(bm);
-    __syncthreads();
-    int rank = __popcll(bm & ((1ull << (tid & 63)) - 1ull));
-    for (int w = 0; w < (tid >> 6); ++w) rank += s_wshared[w];
-    if (tid < ntiles) {
-      int slot = nshared + (tid - rank);  // a per-query tile: after the shared ones
-      if (sh) {
-        // XCD x holds the slots s < nshared with s % 8 == x: c_x of them
-        int first = 0, x = 0;
-        for (; x < kXcds - 1; ++x) {
-          const int c = (nshared - x + kXcds - 1) / kXcds;
-          if (rank < first + c) break;
-          first += c;
-        }
-        slot = kXcds * (rank - first) + x;
+    int k[kOrderPer];
+    keys(0, k, true);
+    int carry = 0;  // shared tiles of the earlier blocks of kThreads tiles
+#pragma unroll
+    for (int u = 0; u < kOrderPlaceMax / kThreads; ++u) {
+      const int t = u * kThreads + tid;
+      const bool sh = k[u] > 0;
+      const unsigned long long bm = __ballot(sh);
+      if (lane == 0) sm.wcount[wave] = __popcll(bm);
+      __syncthreads();
+      int rank = carry + __popcll(bm & below);
+      for (int w = 0; w < kWaves; ++w) {
+        const int c = sm.wcount[w];
+        rank += w < wave ? c : 0;
+        carry += c;
       }
-      p.order[slot] = ((sh ? key(tid) : 0) << kOrderTileBits) | tid;
+      if (t < ntiles) {
+        int slot = nshared + (t - rank);  // a per-query tile: after the shared ones
+        if (sh) {
+          // XCD x holds the slots s < nshared with s % 8 == x: c_x of them
+          int first = 0, x = 0;
+          for (; x < kXcds - 1; ++x) {
+            const int c = (nshared - x + kXcds - 1) / kXcds;
+            if (rank < first + c) break;
+            first += c;
+          }
+          slot = kXcds * (rank - first) + x;
+        }
+        p.order[slot] = ((sh ? k[u] : 0) << kOrderTileBits) | t;
+      }
+      __syncthreads();  // wcount is rewritten by the next block
     }
     return;
   }
-  if (tid < 64) {
+  if (wave == 0) {
     // exclusive scan over descending keys: the start of key k is the number
     // of tiles with a larger key
     int carry = 0;
     for (int c = kOrderKeysPadded / 64 - 1; c >= 0; --c) {
-      const int k = 64 * c + 63 - tid;  // lane 0 takes the largest key of the chunk
-      const int v = s_pos[k];
+      const int k = 64 * c + 63 - lane;  // lane 0 takes the largest key of the chunk
+      const int v = sm.pos[k];
       int incl = v;
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) {
         const int t = __shfl_up(incl, off);
-        if (tid >= off) incl += t;
+        if (lane >= off) incl += t;
       }
-      s_pos[k] = carry + incl - v;
+      sm.pos[k] = carry + incl - v;
       carry += __shfl(incl, 63);
     }
   }
   __syncthreads();
-  for (int t = tid; t < ntiles; t += kOrderThreads) {
-    const int k = key(t);
-    p.order[atomicAdd(&s_pos[k], 1)] = (k << kOrderTileBits) | t;
+  for (int t0 = 0; t0 < ntiles; t0 += kThreads * kOrderPer) {
+    int k[kOrderPer];
+    keys(t0, k, cached);
+#pragma unroll
+    for (int u = 0; u < kOrderPer; ++u) {
+      const int t = t0 + u * kThreads + tid;
+      const unsigned long long z = __ballot(k[u] == 0);
+      int base = 0;
+      if (lane == 0 && z != 0ull) base = atomicAdd(&sm.pos[0], __popcll(z));
+      base = __shfl(base, 0);
+      if (k[u] > 0)
+        p.order[atomicAdd(&sm.pos[k[u]], 1)] = (k[u] << kOrderTileBits) | t;
+      else if (k[u] == 0)
+        p.order[base + __popcll(z & below)] = t;
+    }
+  }
+}
+
+// ============================================================================
+// per-query launch
+// ============================================================================
+// Work-group i runs unit i (query i / nsplit, part i % nsplit). In a
+// shared-row plan (FwdParams::meta set) it runs the queries of one tile in
+// turn if the index kernel made that tile per query, and returns at once
+// otherwise; when the call makes the tile order (FwdParams::ord.order set),
+// work-group 0 makes it and tile i goes to work-group i + 1. (A per-query
+// tile's queries in one work-group take about the CU time the mode rule
+// charges them; short-lived work-groups, one per tile, balance better than
+// fewer that stride over many queries.)
+template <int kRing>
+union QueryLaunchSmem {
+  QuerySmemT<kRing> q;
+  OrderSmem o;
+};
+static_assert(sizeof(OrderSmem) <= sizeof(QuerySmemT<2>), "the order adds no LDS");
+
+// kTiles: the launch of a shared-row plan (FwdParams::meta set); else one
+// unit per work-group (a separate instantiation: the tile-plan loop would
+// cost the plain one scalar-register spills).
+template <int kRing, bool kTiles>
+__global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
+    sa_fwd_query_kernel(const FwdParams p) {
+  __shared__ __attribute__((aligned(16))) QueryLaunchSmem<kRing> sm;
+  if constexpr (!kTiles) {
+    query_unit<kRing>(p, blockIdx.x, sm.q);
+  } else {
+    int64_t t = blockIdx.x;
+    if (p.ord.order != nullptr) {
+      if (t == 0) {
+        make_order(p.ord, sm.o);
+        return;
+      }
+      --t;
+    }
+    if (__builtin_amdgcn_readfirstlane(p.meta[t * kMetaInts + 1]) == kModeShared) return;
+    const int64_t m0 = (t % p.tiles_per_b) * kTQ;
+    const int64_t qbase = (t / p.tiles_per_b) * p.m + m0;
+    const int nq = int(min(int64_t(kTQ), p.m - m0));
+    for (int j = 0; j < nq; ++j) {
+      query_unit<kRing>(p, qbase + j, sm.q);
+      __syncthreads();  // every wave is done with the LDS before the next query
+    }
   }
 }
 
@@ -1072,33 +1193,13 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     const int t = first + int(blockIdx.x) / kXcds;
     const int32_t* mt = p.meta + int64_t(t) * kMetaInts;
     const int nU = __builtin_amdgcn_readfirstlane(mt[0]);
-    if (__builtin_amdgcn_readfirstlane(mt[1]) != kModeShared) {
-      const int64_t b0 = t / p.tiles_per_b;
-      const int64_t m0 = (t % p.tiles_per_b) * kTQ;
-      const int nq = int(min(int64_t(kTQ), p.m - m0));
-      for (int j = 0; j < nq; ++j) {
-        query_unit<4>(p.fwd, b0 * p.m + m0 + j, sm.q);
-        __syncthreads();
-      }
-      return;
-    }
-    entry = int32_t(((1 + (nU + kTileRows - 1) / kTileRows) << kOrderTileBits) | t);
+    const bool shared = __builtin_amdgcn_readfirstlane(mt[1]) == kModeShared;
+    entry = shared ? int32_t(((1 + (nU + kTileRows - 1) / kTileRows) << kOrderTileBits) | t) : 0;
   } else {
-    // one load: tile and step count (work-groups past the order are workers)
-    entry = blockIdx.x < p.ntiles ? p.order[blockIdx.x] : 0;
+    entry = p.order[blockIdx.x];  // one load: tile and step count
   }
-  if ((entry >> kOrderTileBits) == 0) {
-    // Per-query worker: the work-groups from the first per-query tile's
-    // order entry to the end of the grid stride over the work list.
-    const int nq = __builtin_amdgcn_readfirstlane(p.pq[0]);
-    const int nshared = __builtin_amdgcn_readfirstlane(p.pq[1]);
-    const int workers = int(gridDim.x) - nshared;
-    for (int k = int(blockIdx.x) - nshared; k < nq; k += workers) {
-      query_unit<4>(p.fwd, p.pq[2 + k], sm.q);
-      __syncthreads();  // every wave is done with the LDS before the next unit
-    }
-    return;
-  }
+  // a per-query tile: its queries run in the per-query launch
+  if ((entry >> kOrderTileBits) == 0) return;
   const int64_t tile = entry & ((1 << kOrderTileBits) - 1);
   const int nsteps = (entry >> kOrderTileBits) - 1;
   const int64_t bi = tile / p.tiles_per_b;
@@ -1286,7 +1387,8 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       const uint8_t* kr = tb + koff;
       bf16x8 kf[kKRing];
       auto kread = [&](int i, int slot) {
-        kf[slot] = *reinterpret_cast<const bf16x8*>(kr + (i >> 5) * 32 * kTilePitch + 32 * (i & 31));
+        kf[slot] =
+            *reinterpret_cast<const bf16x8*>(kr + (i >> 5) * 32 * kTilePitch + 32 * (i & 31));
       };
 #pragma unroll
       for (int i = 0; i < kKRing - 1; ++i) kread(i, i);
@@ -1753,6 +1855,27 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
   p.split_len = plan.split_len;
   p.nblocks = plan.units * plan.nsplit;
 
+  // The per-query kernel; two work-groups per CU once there are at least two
+  // per CU to run.
+  auto launch_query = [&]() -> int {
+    if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
+    const dim3 grid(unsigned(p.nblocks)), block(kThreads);
+    const bool two = p.nblocks >= 2 * int64_t(cus);
+    if (p.meta != nullptr) {
+      if (two)
+        hipLaunchKernelGGL((sa_fwd_query_kernel<2, true>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((sa_fwd_query_kernel<4, true>), grid, block, 0, stream, p);
+    } else {
+      if (two)
+        hipLaunchKernelGGL((sa_fwd_query_kernel<2, false>), grid, block, 0, stream, p);
+      else
+        hipLaunchKernelGGL((sa_fwd_query_kernel<4, false>), grid, block, 0, stream, p);
+    }
+    if (hipGetLastError() != hipSuccess) return SA_EHIP;
+    return mark(SA_KERNEL_QUERY, 1) ? SA_OK : SA_EHIP;
+  };
+
   if (plan.tiles) {
     IndexParams ip{};
     ip.idx = a->idx;
@@ -1771,16 +1894,17 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     ip.force = (a->flags & SA_FLAG_FORCE_TILES) ? 1 : 0;
     ip.vec4 = ((reinterpret_cast<uintptr_t>(a->idx) & 15u) == 0 && a->topk % 4 == 0 &&
                a->sidx[0] % 4 == 0 && a->sidx[1] % 4 == 0) ? 1 : 0;
+    // from the shape alone, so that an index plan makes the plain call's modes
+    ip.placed_regime = (2 * plan.ntiles >= cus && plan.ntiles <= cus) ? 1 : 0;
     int32_t* order = reinterpret_cast<int32_t*>(ws + plan.order_off);
-    int32_t* pq = reinterpret_cast<int32_t*>(ws + plan.pq_off);
+    const bool planned = what == Launch::kCall && (a->flags & SA_FLAG_PLANNED) != 0;
     // Between half as many tiles as CUs and as many, every tile starts at
-    // once and the order kernel's placement is a formula: the tile kernel
-    // applies it itself and that launch is skipped. (Fewer tiles keep the
-    // order kernel, whose per-query work list spreads the queries of
-    // per-query tiles over every CU. An index plan always holds an order.)
-    const bool placed = (a->flags & SA_FLAG_PLANNED) == 0 && what == Launch::kCall &&
-                        2 * plan.ntiles >= cus && plan.ntiles <= cus;
-    if ((a->flags & SA_FLAG_PLANNED) == 0 || what == Launch::kPlanOnly) {
+    // once and the order's placement is a formula: the tile kernel applies it
+    // itself and no order is made. (Fewer tiles keep the order: with a CU or
+    // more per tile, the longest-first order beats XCD placement. An index
+    // plan always holds an order.)
+    const bool placed = what == Launch::kCall && !planned && ip.placed_regime != 0;
+    if (!planned) {
       const size_t lds = size_t(a->kv_len) * sizeof(unsigned long long);
       if (lds > 65536 &&
           hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
@@ -1792,28 +1916,29 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
       if (hipGetLastError() != hipSuccess) return SA_EHIP;
       if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
     }
-    if (!placed && ((a->flags & SA_FLAG_PLANNED) == 0 || what == Launch::kPlanOnly)) {
-      if (!mark(SA_KERNEL_ORDER, 0)) return SA_EHIP;
-      OrderParams op{};
-      op.meta = ip.meta;
-      op.order = order;
-      op.pq = pq;
-      op.ntiles = int(plan.ntiles);
-      op.m = a->m;
-      op.tiles_per_b = plan.tiles_per_b;
-      op.cus = cus;
-      hipLaunchKernelGGL(sa_tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, stream, op);
-      if (hipGetLastError() != hipSuccess) return SA_EHIP;
-      if (!mark(SA_KERNEL_ORDER, 1)) return SA_EHIP;
+    // The per-query launch: one work-group per tile runs the queries of a
+    // per-query tile (the others return at once), and work-group 0 makes the
+    // tile order when this call makes one (only that, for an index plan).
+    // (Running a placed call's per-query tiles in the tile kernel instead,
+    // through the branch that reruns aborted tiles, makes the compiler spill
+    // the kernel's 256 AGPR accumulators.)
+    p.meta = ip.meta;
+    p.tiles_per_b = plan.tiles_per_b;
+    if (!planned && !placed) {
+      p.ord.meta = ip.meta;
+      p.ord.order = order;
+      p.ord.ntiles = int(plan.ntiles);
+      p.ord.cus = cus;
     }
-    if (what == Launch::kPlanOnly) return SA_OK;
+    p.nblocks = what == Launch::kPlanOnly ? 1 : plan.ntiles + (p.ord.order != nullptr ? 1 : 0);
+    const int lrc = launch_query();
+    if (lrc != SA_OK || what == Launch::kPlanOnly) return lrc;
 
     TileParams tp{};
     tp.q = p.q;
     tp.kv = p.kv;
     tp.sink = a->sink;
     tp.o = p.o;
-    tp.pq = pq;
     tp.order = order;
     tp.row_off = ip.row_off;
     tp.lcnt = ip.lcnt;
@@ -1837,29 +1962,17 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.fwd = p;
     tp.placed = placed ? 1 : 0;
     tp.meta = ip.meta;
-    // Ordered: one work-group per tile, then one per compute unit more: the
-    // queries of per-query tiles are run by the work-groups of those tiles'
-    // order entries and these (an empty work list costs them one read each).
-    // Placed: one work-group per tile.
-    const int64_t grid = placed ? plan.ntiles : plan.ntiles + cus;
+    // One work-group per tile; those of per-query tiles return at once.
     if (!mark(SA_KERNEL_TILE, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(grid)), dim3(kThreads), 0, stream, tp);
+    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), 0,
+                       stream, tp);
     if (hipGetLastError() != hipSuccess) return SA_EHIP;
-    if (!mark(SA_KERNEL_TILE, 1)) return SA_EHIP;
-    return SA_OK;
+    return mark(SA_KERNEL_TILE, 1) ? SA_OK : SA_EHIP;
   }
   if (what == Launch::kPlanOnly) return SA_OK;  // per-query plans keep no index state
 
-  if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
-  // two work-groups per CU once there are at least two per CU to run
-  if (p.nblocks >= 2 * int64_t(cus))
-    hipLaunchKernelGGL(sa_fwd_query_kernel<2>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
-                       stream, p);
-  else
-    hipLaunchKernelGGL(sa_fwd_query_kernel<4>, dim3(unsigned(p.nblocks)), dim3(kThreads), 0,
-                       stream, p);
-  if (hipGetLastError() != hipSuccess) return SA_EHIP;
-  if (!mark(SA_KERNEL_QUERY, 1)) return SA_EHIP;
+  const int lrc = launch_query();
+  if (lrc != SA_OK) return lrc;
   if (plan.nsplit > 1) {
     CombineParams c{};
     c.part = p.part;

@@ -16,7 +16,7 @@ import sa_capi
 _LIB = os.path.join(os.path.dirname(sa_capi.LIB_PATH), "libsa_host_test.so")
 _host = None
 _KEYS = ["nsplit", "split_len", "tiles", "tiles_per_b", "ntiles", "tile_cap", "ws",
-         "meta_off", "order_off", "rows_off", "cnts_off", "pq_off", "part_off"]
+         "meta_off", "order_off", "rows_off", "cnts_off", "part_off"]
 
 
 def device_cus() -> int:

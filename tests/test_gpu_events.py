@@ -24,7 +24,7 @@ def case(b, m, kv_len, topk, seed):
 
 
 @pytest.mark.parametrize("shape,expect", [
-    ((1, 64, 300, 64), INDEX | ORDER | TILE),           # shared-row plan (per-query tiles too)
+    ((1, 64, 300, 64), INDEX | QUERY | TILE),           # shared-row plan (order in QUERY)
     ((4, 1, 2048, 512), QUERY | COMBINE),               # split-topk plan
     ((1, 3, 2048, 64), QUERY),                          # per query, no split
 ])

@@ -119,7 +119,7 @@ def test_plan_of_an_aborting_tile(gpu_sa):
 
 
 @pytest.mark.parametrize("shape,plain,planned", [
-    ((1, 64, 300, 64), INDEX | ORDER | TILE, TILE),
+    ((1, 64, 300, 64), INDEX | QUERY | TILE, QUERY | TILE),
     ((4, 1, 2048, 512), QUERY | COMBINE, QUERY | COMBINE),
     ((1, 3, 2048, 64), QUERY, QUERY),
 ])
@@ -163,8 +163,8 @@ def placed_cases():
                                   "mixed, bad index"])
 def test_placed_tiles_match_ordered(gpu_sa, name):
     """A plain call that places its tiles itself equals the planned call,
-    whose tiles run in the order kernel's placement, bit for bit (o, lse and
-    the error word), and it skips the order kernel."""
+    whose tiles run in the tile order's placement, bit for bit (o, lse and
+    the error word). The plain call makes no tile order."""
     q, kv, sink, idx, sc = placed_cases()[name]()
     if name == "mixed, bad index":
         idx[1, 17, 3] = kv.shape[1] + 5
@@ -192,7 +192,7 @@ def test_placed_tiles_match_ordered(gpu_sa, name):
     expect_plan(q, kv, idx, tiles=True)
     ntiles = q.shape[0] * -(-q.shape[1] // 8)
     assert 2 * ntiles >= cus and ntiles <= cus, "the shape must be in the placed regime"
-    assert k1 == INDEX | TILE and k2 == TILE
+    assert k1 == INDEX | QUERY | TILE and k2 == QUERY | TILE
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     assert e1 == e2 == (1 if name == "mixed, bad index" else 0)
     if name == "high locality":  # and the values themselves, on a sample

@@ -173,12 +173,12 @@ def test_tiles_deterministic(gpu_sa):
     assert torch.equal(a, b)
 
 
-def test_per_query_work_list_matches_direct_launch(gpu_sa):
-    """A tile plan whose tiles all go to the per-query kernel (low overlap):
-    the kernel strides over the work list the order kernel writes, one
-    work-group per CU, several queries per work-group on 256 CUs, a
-    ragged last tile. Each query must equal the direct per-query launch
-    bit for bit, and the sampled oracle check must pass."""
+def test_per_query_tiles_match_direct_launch(gpu_sa):
+    """A tile plan whose tiles all go per query (low overlap): the per-query
+    launch after the shared-row kernel runs them, one work-group per query
+    of the plan reading its tile's mode, with a ragged last tile. Each query
+    must equal the direct per-query launch bit for bit, and the sampled
+    oracle check must pass."""
     q, kv, sink, idx, sc = rand_case(1, 300, 16384, 256, seed=21, minus1=0.1)
     expect_plan(q, kv, idx, 0, tiles=True, nsplit=1)
     o_l = run(q, kv, sink, idx, sc)
@@ -189,14 +189,45 @@ def test_per_query_work_list_matches_direct_launch(gpu_sa):
     d = (o_l.float() - o_p.float()).abs()
     assert d.max().item() <= 2e-2
     sampled_check(o_l, q, kv, sink, idx, sc, [(0, t) for t in (0, 1, 150, 295, 296, 299)],
-                  "work list")
+                  "per-query tiles")
 
 
-def test_work_list_mixed_with_aborted_tile(gpu_sa):
+def mixed_many_tiles(seed):
+    """2 x 4400 queries (1100 tiles, more than the order kernel's 1024
+    threads), every third tile of overlapping windows (shared), the others
+    128 random rows of 4096 (per query), ragged last tiles."""
+    q, kv, sink, idx, sc = rand_case(2, 4400, 4096, 128, seed=seed)
+    t = torch.arange(4400)
+    win = ((torch.arange(128)[None] + 3 * t[:, None]) % 4096).to(torch.int32)
+    sel = (t // 8) % 3 == 0
+    idx[:, sel] = win[sel]
+    return q, kv, sink, idx, sc, sel
+
+
+def test_per_query_tiles_strided_over_many_tiles(gpu_sa):
+    """The per-query launch after the shared-row kernel strides over the
+    per-query tiles' queries, which the order kernel lists in tile order after
+    the shared tiles: those queries equal the direct per-query launch bit for
+    bit, the shared tiles' agree within the tolerance, and a sample matches
+    the oracle."""
+    q, kv, sink, idx, sc, sel = mixed_many_tiles(seed=31)
+    expect_plan(q, kv, idx, 0, tiles=True, nsplit=1)
+    o = run(q, kv, sink, idx, sc).cpu()
+    o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY).cpu()
+    assert torch.equal(o[:, ~sel], o_p[:, ~sel])
+    d = (o.float() - o_p.float()).abs()
+    say(f"  strided per-query tiles: max {d.max().item():.3e}")
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
+    sampled_check(o, q, kv, sink, idx, sc,
+                  [(0, 0), (0, 9), (1, 23), (1, 2401), (0, 4391), (1, 4399)], "strided")
+
+
+def test_per_query_tiles_mixed_with_aborted_tile(gpu_sa):
     """Shared tiles, per-query tiles from the index kernel and a tile that
     aborts at run time (scores jump far above its reference) in one call: the
-    aborted tile's queries are appended to the work list by the tile kernel
-    and computed by the per-query kernel launched next."""
+    aborted tile's work-group runs its queries per query itself, and the
+    per-query tiles' queries run in the per-query launch after the shared-row
+    kernel."""
     # 256 queries (the plan must not split them); 512 random rows of 8192 per
     # query leave a tile's dense work ~7.6x its valid slots, so those tiles go
     # to the per-query kernel

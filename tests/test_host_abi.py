@@ -155,7 +155,7 @@ def test_library_exports_every_declared_symbol(libs):
     hip, _ = libs
     for name in declared_functions():
         assert hasattr(hip, name), f"{name} not exported"
-    assert hip.sa_abi_version() == 4
+    assert hip.sa_abi_version() == 5
 
 
 def test_strerror_covers_codes(libs):
@@ -251,10 +251,10 @@ PART_BYTES = 2 * 16 * 4 + 16 * 512 * 4
 
 
 def plan_full(host, a, cus):
-    out = (ctypes.c_int64 * 13)()
+    out = (ctypes.c_int64 * 12)()
     assert host.sa_host_plan_full(ctypes.byref(a), cus, out) == SA_OK
     keys = ["nsplit", "split_len", "tiles", "tiles_per_b", "ntiles", "tile_cap", "ws",
-            "meta_off", "order_off", "rows_off", "cnts_off", "pq_off", "part_off"]
+            "meta_off", "order_off", "rows_off", "cnts_off", "part_off"]
     return dict(zip(keys, list(out)))
 
 
@@ -284,14 +284,11 @@ def test_tile_plan(libs, b, m, kv_len, topk, flags, tiles):
         assert p["tiles_per_b"] == -(-m // 8) and p["ntiles"] == b * p["tiles_per_b"]
         assert p["tile_cap"] % 64 == 0 and p["tile_cap"] >= min(kv_len, 8 * topk)
         # per tile: meta, its slot in the launch order, a 32-bit offset per
-        # union row and an fp16 log2 multiplicity per (query, union row); then
-        # the per-query work list (a count, the shared-tile count and up to
-        # b * m query ids)
-        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 2 * 8) * p["tile_cap"]) + 4 * (2 + b * m)
+        # union row and an fp16 log2 multiplicity per (query, union row)
+        assert p["ws"] >= p["ntiles"] * (16 + 4 + (4 + 2 * 8) * p["tile_cap"])
         regions = [(p["meta_off"], 16 * p["ntiles"]), (p["order_off"], 4 * p["ntiles"]),
                    (p["rows_off"], 4 * p["ntiles"] * p["tile_cap"]),
-                   (p["cnts_off"], 2 * 8 * p["ntiles"] * p["tile_cap"]),
-                   (p["pq_off"], 4 * (2 + b * m))]
+                   (p["cnts_off"], 2 * 8 * p["ntiles"] * p["tile_cap"])]
         for (o0, n0), (o1, _) in zip(regions, regions[1:]):
             assert o0 % 256 == 0 and o0 + n0 <= o1           # aligned, disjoint, in order
         assert regions[-1][0] + regions[-1][1] <= p["ws"]
