@@ -387,6 +387,7 @@ struct QuerySmemT {
   __bf16 p[kHeads * kQRows];
   float red[kWaves][kHeads];
   int cnt[kWaves];
+  int qstart[kTQ + 1];  // query_stream: query j's entries of `list` start here
 };
 using QuerySmem = QuerySmemT<4>;
 static_assert(sizeof(QuerySmemT<2>) <= 80 * 1024, "two ring-2 work-groups per CU");
@@ -403,6 +404,205 @@ __device__ __forceinline__ void wait_ring(int later) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+// Per-query kernel state of one (query, part) for this lane: the running max
+// (log2 domain) and this lane's share of the running sum of head n, O, and
+// Q^T as the B operand of S^T = K . Q^T (lane (n, g) holds head n,
+// d = 32s + 8g .. 32s + 8g + 7 for k-step s).
+struct QueryState {
+  float m_run;
+  float l_run;
+  f32x4 oacc[kDBlocks];
+  bf16x8 qf[kDim / 32];
+};
+
+__device__ __forceinline__ void query_state_reset(QueryState& st) {
+  st.m_run = -INFINITY;
+  st.l_run = 0.f;
+#pragma unroll
+  for (int i = 0; i < kDBlocks; ++i) st.oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
+// Issues the loads of query (bi, mi)'s Q^T into st.qf.
+__device__ __forceinline__ void query_load_q(const FwdParams& p, int64_t bi, int64_t mi,
+                                             QueryState& st) {
+  const int lane = threadIdx.x & 63;
+  const __bf16* qrow = p.q + bi * p.sq_b + mi * p.sq_m + int64_t(lane & 15) * p.sq_h +
+                       8 * (lane >> 4);
+#pragma unroll
+  for (int s = 0; s < kDim / 32; ++s) st.qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+}
+
+// One step of the per-query kernel over the 32 rows in LDS buffer `tb`, of
+// which the first `nrows` are valid (at least one): S^T for this wave's 8
+// rows, the online softmax (per-head max across the waves through LDS), and
+// O += P . V. When `dma`, this wave's 8 gathers of a later step (rows
+// readlane(rv, i) of `kvb`, into LDS at lbase + i * kRowStride) ride between
+// the S^T MFMAs. `after_s` runs once S^T is done (Q^T is no longer read).
+template <int kRing, typename AfterS>
+__device__ __forceinline__ void query_step(const FwdParams& p, QuerySmemT<kRing>& sm,
+                                           const uint8_t* tb, bool dma, int rv, uint32_t lbase,
+                                           const uint8_t* kvb, int64_t row_bytes, int nrows,
+                                           QueryState& st, AfterS after_s) {
+  auto& s_p = sm.p;
+  auto& s_red = sm.red;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15;   // MFMA column lane: head (S^T, P) or d (O)
+  const int g = lane >> 4;   // MFMA k-group
+  float& m_run = st.m_run;
+  float& l_run = st.l_run;
+  auto& oacc = st.oacc;
+  const auto& qf = st.qf;
+
+  // ---- S^T = K . Q^T for this wave's 8 rows ----------------------------------
+  // MFMA rows 8..15 repeat rows 0..7 (the A operand reads row n & 7). The K
+  // fragments are read 3 MFMAs ahead; the 8 row gathers of the later step
+  // ride between the MFMAs (one after every second), where their issue cost
+  // overlaps the MFMA chain.
+  f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
+  {
+    const uint8_t* krow = tb + (wave * kQRowsPerWave + (n & 7)) * kRowStride + 16 * g;
+    auto s_chain = [&](auto with_dma) {
+      bf16x8 kf[4];
+#pragma unroll
+      for (int s = 0; s < 3; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 64 * s);
+#pragma unroll
+      for (int s = 0; s < kDim / 32; ++s) {
+        if (s + 3 < kDim / 32)
+          kf[(s + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (s + 3));
+        sacc = mfma_16x16x32(kf[s & 3], qf[s], sacc);
+        if constexpr (decltype(with_dma)::value) {
+          if (s & 1) {
+            const int i = s >> 1;
+            const int row = __builtin_amdgcn_readlane(rv, i);
+            lds_dma_row(kvb + int64_t(row) * row_bytes, 16 * lane,
+                        lbase + uint32_t(i * kRowStride));
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the interleave
+      }
+    };
+    static_assert(kDim / 32 == 2 * kQRowsPerWave, "one gather per two S^T MFMAs");
+    if (dma)
+      s_chain(std::true_type{});
+    else
+      s_chain(std::false_type{});
+  }
+  after_s();
+  // lane (n, g) now holds S[head n][row 8w + 4g + j], j = 0..3; lanes with
+  // g >= 2 hold the repeated rows and drop them
+
+  // ---- online softmax ------------------------------------------------------
+  const int rbase = wave * kQRowsPerWave + 4 * g;  // row within the step
+  float sv[4];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sv[j] = (g < 2 && rbase + j < nrows) ? sacc[j] * p.scale_log2 : -INFINITY;
+    mx = fmaxf(mx, sv[j]);
+  }
+  mx = wave_max16(mx);
+  if (g == 0) s_red[wave][n] = mx;
+  lds_barrier();
+  // finite: the step's first row is valid (wave 0)
+  const float mstep = fmaxf(fmaxf(s_red[0][n], s_red[1][n]), fmaxf(s_red[2][n], s_red[3][n]));
+  float alpha = 1.f;
+  if (mstep > m_run + kRescaleLog2) {
+    alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mstep);  // O, l still 0 at first
+    m_run = mstep;
+  }
+  float psum = 0.f;
+  bf16x4 pb;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float pj = exp2f(sv[j] - m_run);
+    psum += pj;
+    pb[j] = static_cast<__bf16>(pj);
+  }
+  l_run = l_run * alpha + psum;
+  if (g < 2) *reinterpret_cast<bf16x4*>(&s_p[n * kQRows + wave * kQRowsPerWave + 4 * g]) = pb;
+  if (__any(alpha != 1.f)) {
+    float aj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) aj[j] = __shfl(alpha, 4 * g + j);
+#pragma unroll
+    for (int blk = 0; blk < kDBlocks; ++blk)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) oacc[blk][j] *= aj[j];
+  }
+  lds_barrier();  // P of every wave is in LDS
+
+  // ---- O[:, 128w .. 128w+127] += P . V over the step's 32 rows ---------------
+  {
+    const bf16x8 pf = *reinterpret_cast<const bf16x8*>(&s_p[n * kQRows + 8 * g]);
+    const uint8_t* vb =
+        tb + (8 * g + (n >> 2)) * kRowStride + (wave * kDPerWave + 4 * (n & 3)) * 2;
+#pragma unroll
+    for (int blk = 0; blk < kDBlocks; ++blk) {
+      const bf16x4 v0 = lds_read_tr16(vb + blk * 32);
+      const bf16x4 v1 = lds_read_tr16(vb + 4 * kRowStride + blk * 32);
+      const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+      oacc[blk] = mfma_16x16x32(pf, vf, oacc[blk]);
+    }
+  }
+}
+
+// The end of a (query, part) unit: the running sum across the waves, then
+// bf16 o (and lse) with the sink folded in, or this part's (max, sum,
+// unnormalised O) for the combine kernel when the query is split. Every wave
+// is past its LDS accesses only after the work-group's final barrier here.
+template <int kRing>
+__device__ __forceinline__ void query_epilogue(const FwdParams& p, QuerySmemT<kRing>& sm,
+                                               int64_t unit, int64_t bi, int64_t mi,
+                                               const QueryState& st) {
+  auto& s_red = sm.red;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const float m_run = st.m_run;
+  const float l_run = st.l_run;
+  const auto& oacc = st.oacc;
+  float lw = wave_sum16(l_run);
+  __syncthreads();
+  if (g == 0) s_red[wave][n] = lw;
+  __syncthreads();
+  const float l_tot = s_red[0][n] + s_red[1][n] + s_red[2][n] + s_red[3][n];
+  const int dcol = wave * kDPerWave + n;
+
+  if (p.nsplit == 1) {
+    float lse;
+    const float f = sink_fold(m_run, l_tot, p.sink[n] * kLog2e, lse);
+    if (p.lse != nullptr && wave == 0 && g == 0)
+      p.lse[bi * p.sl_b + mi * p.sl_m + int64_t(n) * p.sl_h] = lse;
+    float fj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) fj[j] = __shfl(f, 4 * g + j);
+    __bf16* ob = p.o + bi * p.so_b + mi * p.so_m;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      __bf16* orow = ob + int64_t(4 * g + j) * p.so_h + dcol;
+#pragma unroll
+      for (int blk = 0; blk < kDBlocks; ++blk)
+        orow[16 * blk] = static_cast<__bf16>(oacc[blk][j] * fj[j]);
+    }
+  } else {
+    float* part = p.part + unit * kPartFloats;
+    if (wave == 0 && g == 0) {
+      part[n] = m_run;
+      part[kHeads + n] = l_tot;
+    }
+    float* po = part + 2 * kHeads;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int blk = 0; blk < kDBlocks; ++blk)
+        po[(4 * g + j) * kDim + dcol + 16 * blk] = oacc[blk][j];
+  }
+}
+
 // One (query, topk part) unit of the per-query kernel. Leaves every wave past
 // its last LDS access of `sm` only after the work-group's final barrier, so a
 // following unit may reuse `sm` after one more __syncthreads().
@@ -413,15 +613,11 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
   constexpr int kQAhead = kRing - 1;
   static_assert(kQAhead >= 1 && kQAhead <= 3, "wait_ring covers up to 2 later steps");
   auto& s_list = sm.list;
-  auto& s_p = sm.p;
-  auto& s_red = sm.red;
   auto& s_cnt = sm.cnt;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = lane & 15;   // MFMA column lane: head (S^T, P) or d (O)
-  const int g = lane >> 4;   // MFMA k-group
 
   const int64_t qid = unit / p.nsplit;
   const int split = int(unit % p.nsplit);
@@ -437,13 +633,8 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
   const uint32_t lds_rows = __builtin_amdgcn_readfirstlane(uint32_t(
       reinterpret_cast<uintptr_t>((lds_u8_t*)&sm.tile[0][wave * kQRowsPerWave * kRowStride])));
 
-  float m_run = -INFINITY;  // running max (log2 domain) of head n
-  float l_run = 0.f;        // this lane's share of the running sum of head n
-  f32x4 oacc[kDBlocks];
-#pragma unroll
-  for (int i = 0; i < kDBlocks; ++i) oacc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  bf16x8 qf[kDim / 32];
+  QueryState st;
+  query_state_reset(st);
   for (int64_t base = s_begin; base < s_end; base += kListCap) {
     const int cnt = int(min(int64_t(kListCap), s_end - base));
     __syncthreads();  // the previous batch is done with s_list and the ring
@@ -457,18 +648,12 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
       const int sl = tid * kSlotsPerThread + i;
       raw[i] = sl < cnt ? irow[base + sl] : -1;
     }
-    {
-      // Q^T as the B operand of S^T = K . Q^T: lane (n, g) holds head n,
-      // d = 32s + 8g .. 32s + 8g + 7 for k-step s. Issued after the index
-      // loads (which return first, so the compaction waits for them alone)
-      // and complete before the first gather is issued (vmcnt below). Not
-      // under a branch, so that the compiler's wait for the indices counts
-      // these loads as younger; a batch after the first reloads the same Q.
-      const __bf16* qrow = p.q + bi * p.sq_b + mi * p.sq_m + int64_t(n) * p.sq_h + 8 * g;
-#pragma unroll
-      for (int s = 0; s < kDim / 32; ++s)
-        qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
-    }
+    // Q^T: issued after the index loads (which return first, so the
+    // compaction waits for them alone) and complete before the first gather
+    // is issued (vmcnt below). Not under a branch, so that the compiler's
+    // wait for the indices counts these loads as younger; a batch after the
+    // first reloads the same Q.
+    query_load_q(p, bi, mi, st);
 #pragma unroll
     for (int i = 0; i < kSlotsPerThread; ++i) {
       const int v = raw[i];
@@ -523,7 +708,6 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
     for (int step = 0; step < nsteps; ++step) {
       wait_ring(min(nsteps - 1, step + kQAhead - 1) - step);
       lds_barrier();  // every wave's rows of `step` are in LDS; the previous buffer is free
-      const uint8_t* tb = sm.tile[step % kQRing];
       // the list entries of the rows this wave gathers for step + kQAhead
       const int sg = step + kQAhead;
       int rv = 0;
@@ -532,139 +716,170 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
         rv = s_list[e < nvalid ? e : 0];
       }
       const uint32_t lbase = lds_rows + uint32_t((sg % kQRing) * kQRows * kRowStride);
-
-      // ---- S^T = K . Q^T for this wave's 8 rows ----------------------------------
-      // MFMA rows 8..15 repeat rows 0..7 (the A operand reads row n & 7). The K
-      // fragments are read 3 MFMAs ahead; the 8 row gathers of step +
-      // kQAhead ride between the MFMAs (one after every second), where their
-      // issue cost overlaps the MFMA chain.
-      f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-      {
-        const uint8_t* krow = tb + (wave * kQRowsPerWave + (n & 7)) * kRowStride + 16 * g;
-        auto s_chain = [&](auto with_dma) {
-          bf16x8 kf[4];
-#pragma unroll
-          for (int s = 0; s < 3; ++s) kf[s] = *reinterpret_cast<const bf16x8*>(krow + 64 * s);
-#pragma unroll
-          for (int s = 0; s < kDim / 32; ++s) {
-            if (s + 3 < kDim / 32)
-              kf[(s + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (s + 3));
-            sacc = mfma_16x16x32(kf[s & 3], qf[s], sacc);
-            if constexpr (decltype(with_dma)::value) {
-              if (s & 1) {
-                const int i = s >> 1;
-                const int row = __builtin_amdgcn_readlane(rv, i);
-                lds_dma_row(kvb + int64_t(row) * row_bytes, 16 * lane,
-                            lbase + uint32_t(i * kRowStride));
-              }
-            }
-            __builtin_amdgcn_sched_barrier(0);  // keep the interleave
-          }
-        };
-        static_assert(kDim / 32 == 2 * kQRowsPerWave, "one gather per two S^T MFMAs");
-        if (sg < nsteps)
-          s_chain(std::true_type{});
-        else
-          s_chain(std::false_type{});
-      }
-      // lane (n, g) now holds S[head n][row 8w + 4g + j], j = 0..3; lanes with
-      // g >= 2 hold the repeated rows and drop them
-
-      // ---- online softmax ------------------------------------------------------
-      const int rbase = step * kQRows + wave * kQRowsPerWave + 4 * g;
-      float sv[4];
-      float mx = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sv[j] = (g < 2 && rbase + j < nvalid) ? sacc[j] * p.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sv[j]);
-      }
-      mx = wave_max16(mx);
-      if (g == 0) s_red[wave][n] = mx;
-      lds_barrier();
-      // finite: the step's first row is valid (wave 0)
-      const float mstep = fmaxf(fmaxf(s_red[0][n], s_red[1][n]), fmaxf(s_red[2][n], s_red[3][n]));
-      float alpha = 1.f;
-      if (mstep > m_run + kRescaleLog2) {
-        alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mstep);  // O, l still 0 at first
-        m_run = mstep;
-      }
-      float psum = 0.f;
-      bf16x4 pb;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float pj = exp2f(sv[j] - m_run);
-        psum += pj;
-        pb[j] = static_cast<__bf16>(pj);
-      }
-      l_run = l_run * alpha + psum;
-      if (g < 2) *reinterpret_cast<bf16x4*>(&s_p[n * kQRows + wave * kQRowsPerWave + 4 * g]) = pb;
-      if (__any(alpha != 1.f)) {
-        float aj[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) aj[j] = __shfl(alpha, 4 * g + j);
-#pragma unroll
-        for (int blk = 0; blk < kDBlocks; ++blk)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) oacc[blk][j] *= aj[j];
-      }
-      lds_barrier();  // P of every wave is in LDS
-
-      // ---- O[:, 128w .. 128w+127] += P . V over the step's 32 rows ---------------
-      {
-        const bf16x8 pf = *reinterpret_cast<const bf16x8*>(&s_p[n * kQRows + 8 * g]);
-        const uint8_t* vb =
-            tb + (8 * g + (n >> 2)) * kRowStride + (wave * kDPerWave + 4 * (n & 3)) * 2;
-#pragma unroll
-        for (int blk = 0; blk < kDBlocks; ++blk) {
-          const bf16x4 v0 = lds_read_tr16(vb + blk * 32);
-          const bf16x4 v1 = lds_read_tr16(vb + 4 * kRowStride + blk * 32);
-          const bf16x8 vf = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-          oacc[blk] = mfma_16x16x32(pf, vf, oacc[blk]);
-        }
-      }
+      query_step<kRing>(p, sm, sm.tile[step % kQRing], sg < nsteps, rv, lbase, kvb, row_bytes,
+                        nvalid - step * kQRows, st, [] {});
     }
   }
-
-  // ---- epilogue ---------------------------------------------------------------
-  float lw = wave_sum16(l_run);
-  __syncthreads();
-  if (g == 0) s_red[wave][n] = lw;
-  __syncthreads();
-  const float l_tot = s_red[0][n] + s_red[1][n] + s_red[2][n] + s_red[3][n];
-  const int dcol = wave * kDPerWave + n;
-
-  if (p.nsplit == 1) {
-    float lse;
-    const float f = sink_fold(m_run, l_tot, p.sink[n] * kLog2e, lse);
-    if (p.lse != nullptr && wave == 0 && g == 0)
-      p.lse[bi * p.sl_b + mi * p.sl_m + int64_t(n) * p.sl_h] = lse;
-    float fj[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) fj[j] = __shfl(f, 4 * g + j);
-    __bf16* ob = p.o + bi * p.so_b + mi * p.so_m;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      __bf16* orow = ob + int64_t(4 * g + j) * p.so_h + dcol;
-#pragma unroll
-      for (int blk = 0; blk < kDBlocks; ++blk)
-        orow[16 * blk] = static_cast<__bf16>(oacc[blk][j] * fj[j]);
-    }
-  } else {
-    float* part = p.part + unit * kPartFloats;
-    if (wave == 0 && g == 0) {
-      part[n] = m_run;
-      part[kHeads + n] = l_tot;
-    }
-    float* po = part + 2 * kHeads;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int blk = 0; blk < kDBlocks; ++blk)
-        po[(4 * g + j) * kDim + dcol + 16 * blk] = oacc[blk][j];
-  }
+  query_epilogue<kRing>(p, sm, unit, bi, mi, st);
 }
 
+// The queries m0 .. m0 + nq - 1 of batch bi (nq <= kTQ, nq * topk <= kListCap,
+// no split) as one stream of steps through a 2-deep ring. Their valid slots
+// are compacted into the list at once (query j's at qs[j] .. qs[j + 1]), so
+// a query's first gathers are issued during the previous query's last step
+// and its Q^T loads once that step's S^T is done: the index loads, the
+// compaction and the first gather latency are paid once per tile instead of
+// once per query.
+// The compiler does not see the LDS-DMA gathers, so every step's ring wait
+// (vmcnt(0) with 2 buffers) is also made as a builtin the compiler sees: its
+// count of outstanding loads then never holds a Q^T load, and it puts no wait
+// of its own between the gathers of a step.
+template <int kRing>
+__device__ __forceinline__ void query_stream(const FwdParams& p, int64_t bi, int64_t m0, int nq,
+                                             QuerySmemT<kRing>& sm) {
+  static_assert(kRing == 2, "the stream's waits are those of a 2-deep ring");
+  constexpr int kQAhead = kRing - 1;
+  auto& s_list = sm.list;
+  auto& s_cnt = sm.cnt;
+  auto& s_qs = sm.qstart;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int topk = int(p.topk);
+  const int nslots = nq * topk;
+  const uint8_t* kvb = reinterpret_cast<const uint8_t*>(p.kv + bi * p.skv_b);
+  const int64_t row_bytes = p.skv_n * 2;
+  const int32_t* ib = p.idx + bi * p.si_b + m0 * p.si_m;
+  const uint32_t lds_rows = __builtin_amdgcn_readfirstlane(uint32_t(
+      reinterpret_cast<uintptr_t>((lds_u8_t*)&sm.tile[0][wave * kQRowsPerWave * kRowStride])));
+
+  // ---- compaction of the tile's valid slots, query by query -------------------
+  // thread tid holds slots tid * kSlotsPerThread + i: query j0 + .., slot k0 + ..
+  const int sl0 = tid * kSlotsPerThread;
+  const int j0 = sl0 / topk;
+  const int k0 = sl0 - j0 * topk;
+  int raw[kSlotsPerThread];
+  {
+    int j = j0, k = k0;
+#pragma unroll
+    for (int i = 0; i < kSlotsPerThread; ++i) {
+      raw[i] = sl0 + i < nslots ? ib[j * p.si_m + k] : -1;
+      if (++k == topk) {
+        k = 0;
+        ++j;
+      }
+    }
+  }
+  QueryState st;
+  query_state_reset(st);
+  query_load_q(p, bi, m0, st);  // query 0's (reloaded below if it has no valid slot)
+  int vals[kSlotsPerThread];
+  int c = 0;
+  bool bad = false;
+#pragma unroll
+  for (int i = 0; i < kSlotsPerThread; ++i) {
+    const int v = raw[i];
+    const bool ok = (v >= 0) && (int64_t(v) < p.kv_len);
+    bad |= (!ok && v != -1);
+    vals[i] = ok ? v : -1;
+    c += ok ? 1 : 0;
+  }
+  if (bad && p.err != nullptr) flag_bad_index(p.err);
+  int incl = c;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  if (lane == 63) s_cnt[wave] = incl;
+  __syncthreads();
+  int pos = incl - c;
+  int nvalid = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const int t = s_cnt[w];
+    pos += (w < wave) ? t : 0;
+    nvalid += t;
+  }
+  {
+    int j = j0, k = k0;
+#pragma unroll
+    for (int i = 0; i < kSlotsPerThread; ++i) {
+      if (k == 0 && sl0 + i < nslots) s_qs[j] = pos;  // a query's first slot
+      if (vals[i] >= 0) s_list[pos++] = vals[i];
+      if (++k == topk) {
+        k = 0;
+        ++j;
+      }
+    }
+  }
+  if (tid == 0) s_qs[nq] = nvalid;
+  __syncthreads();
+  int qs[kTQ + 1];
+#pragma unroll
+  for (int j = 0; j <= kTQ; ++j) qs[j] = j <= nq ? __builtin_amdgcn_readfirstlane(s_qs[j]) : nvalid;
+  auto nst = [&](int j) { return (qs[j + 1] - qs[j] + kQRows - 1) / kQRows; };
+  int total = 0;
+#pragma unroll
+  for (int j = 0; j < kTQ; ++j) total += j < nq ? nst(j) : 0;
+  // Q^T (and the indices) complete before the first gather is issued
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
+  // ---- the step stream ----------------------------------------------------------
+  // The issue cursor (ji, si): query and step of the next step to gather.
+  // Entries past a query's last valid one take its first entry's row; their
+  // scores are masked.
+  int ji = 0, si = 0;
+  while (ji < nq && nst(ji) == 0) ++ji;
+  auto cursor_rows = [&]() {
+    const int e = qs[ji] + si * kQRows + wave * kQRowsPerWave + (lane & 7);
+    const int rv = s_list[e < qs[ji + 1] ? e : qs[ji]];
+    if (++si == nst(ji)) {
+      si = 0;
+      do {
+        ++ji;
+      } while (ji < nq && nst(ji) == 0);
+    }
+    return rv;
+  };
+  if (total > 0) {
+    const int rv = cursor_rows();
+#pragma unroll
+    for (int i = 0; i < kQRowsPerWave; ++i) {
+      const int row = __builtin_amdgcn_readlane(rv, i);
+      lds_dma_row(kvb + int64_t(row) * row_bytes, 16 * lane, lds_rows + uint32_t(i * kRowStride));
+    }
+  }
+  int gstep = 0;
+  int qloaded = 0;  // the query whose Q^T is in st.qf
+  for (int j = 0; j < nq; ++j) {
+    const int ns = nst(j);
+    int jn = j + 1;  // the next query with a valid slot
+    while (jn < nq && nst(jn) == 0) ++jn;
+    if (ns > 0 && qloaded != j) {  // only after a query without a valid slot
+      query_load_q(p, bi, m0 + j, st);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      qloaded = j;
+    }
+    for (int s = 0; s < ns; ++s, ++gstep) {
+      wait_ring(0);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // the same wait, for the compiler's count
+      lds_barrier();  // every wave's rows of this step are in LDS; the other buffer is free
+      const bool dma = gstep + kQAhead < total;
+      const int rv = dma ? cursor_rows() : 0;
+      const uint32_t lbase =
+          lds_rows + uint32_t(((gstep + kQAhead) % kRing) * kQRows * kRowStride);
+      const bool last = s == ns - 1;
+      query_step<kRing>(p, sm, sm.tile[gstep % kRing], dma, rv, lbase, kvb, row_bytes,
+                        qs[j + 1] - qs[j] - s * kQRows, st, [&] {
+                          if (last && jn < nq) query_load_q(p, bi, m0 + jn, st);
+                        });
+    }
+    if (ns > 0 && jn < nq) qloaded = jn;
+    query_epilogue<kRing>(p, sm, bi * p.m + m0 + j, bi, m0 + j, st);
+    query_state_reset(st);
+  }
+}
 
 // ============================================================================
 // tile index kernel
@@ -1110,6 +1325,12 @@ __global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
     const int64_t m0 = (t % p.tiles_per_b) * kTQ;
     const int64_t qbase = (t / p.tiles_per_b) * p.m + m0;
     const int nq = int(min(int64_t(kTQ), p.m - m0));
+    if constexpr (kRing == 2) {
+      if (int64_t(nq) * p.topk <= kListCap) {
+        query_stream<kRing>(p, t / p.tiles_per_b, m0, nq, sm.q);
+        return;
+      }
+    }
     for (int j = 0; j < nq; ++j) {
       query_unit<kRing>(p, qbase + j, sm.q);
       __syncthreads();  // every wave is done with the LDS before the next query
