@@ -437,8 +437,10 @@ __device__ __forceinline__ void query_load_q(const FwdParams& p, int64_t bi, int
 // rows, the online softmax (per-head max across the waves through LDS), and
 // O += P . V. When `dma`, this wave's 8 gathers of a later step (rows
 // readlane(rv, i) of `kvb`, into LDS at lbase + i * kRowStride) ride between
-// the S^T MFMAs. `after_s` runs once S^T is done (Q^T is no longer read).
-template <int kRing, typename AfterS>
+// the S^T MFMAs; with kByteOffsets, rv holds the rows' 32-bit byte offsets
+// in `kvb` instead (one scalar add per address instead of a 64-bit
+// multiply). `after_s` runs once S^T is done (Q^T is no longer read).
+template <int kRing, bool kByteOffsets = false, typename AfterS>
 __device__ __forceinline__ void query_step(const FwdParams& p, QuerySmemT<kRing>& sm,
                                            const uint8_t* tb, bool dma, int rv, uint32_t lbase,
                                            const uint8_t* kvb, int64_t row_bytes, int nrows,
@@ -476,8 +478,9 @@ __device__ __forceinline__ void query_step(const FwdParams& p, QuerySmemT<kRing>
           if (s & 1) {
             const int i = s >> 1;
             const int row = __builtin_amdgcn_readlane(rv, i);
-            lds_dma_row(kvb + int64_t(row) * row_bytes, 16 * lane,
-                        lbase + uint32_t(i * kRowStride));
+            const uint8_t* src =
+                kByteOffsets ? kvb + uint32_t(row) : kvb + int64_t(row) * row_bytes;
+            lds_dma_row(src, 16 * lane, lbase + uint32_t(i * kRowStride));
           }
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the interleave
@@ -729,7 +732,8 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
 // a query's first gathers are issued during the previous query's last step
 // and its Q^T loads once that step's S^T is done: the index loads, the
 // compaction and the first gather latency are paid once per tile instead of
-// once per query.
+// once per query. The list holds the rows' 32-bit byte offsets in the
+// batch's kv (a shared-row plan guarantees they fit).
 // The compiler does not see the LDS-DMA gathers, so every step's ring wait
 // (vmcnt(0) with 2 buffers) is also made as a builtin the compiler sees: its
 // count of outstanding loads then never holds a Q^T load, and it puts no wait
@@ -806,7 +810,7 @@ __device__ __forceinline__ void query_stream(const FwdParams& p, int64_t bi, int
 #pragma unroll
     for (int i = 0; i < kSlotsPerThread; ++i) {
       if (k == 0 && sl0 + i < nslots) s_qs[j] = pos;  // a query's first slot
-      if (vals[i] >= 0) s_list[pos++] = vals[i];
+      if (vals[i] >= 0) s_list[pos++] = int32_t(uint32_t(vals[i]) * uint32_t(row_bytes));
       if (++k == topk) {
         k = 0;
         ++j;
@@ -846,8 +850,8 @@ __device__ __forceinline__ void query_stream(const FwdParams& p, int64_t bi, int
     const int rv = cursor_rows();
 #pragma unroll
     for (int i = 0; i < kQRowsPerWave; ++i) {
-      const int row = __builtin_amdgcn_readlane(rv, i);
-      lds_dma_row(kvb + int64_t(row) * row_bytes, 16 * lane, lds_rows + uint32_t(i * kRowStride));
+      const uint32_t off = uint32_t(__builtin_amdgcn_readlane(rv, i));
+      lds_dma_row(kvb + off, 16 * lane, lds_rows + uint32_t(i * kRowStride));
     }
   }
   int gstep = 0;
@@ -870,10 +874,10 @@ __device__ __forceinline__ void query_stream(const FwdParams& p, int64_t bi, int
       const uint32_t lbase =
           lds_rows + uint32_t(((gstep + kQAhead) % kRing) * kQRows * kRowStride);
       const bool last = s == ns - 1;
-      query_step<kRing>(p, sm, sm.tile[gstep % kRing], dma, rv, lbase, kvb, row_bytes,
-                        qs[j + 1] - qs[j] - s * kQRows, st, [&] {
-                          if (last && jn < nq) query_load_q(p, bi, m0 + jn, st);
-                        });
+      query_step<kRing, true>(p, sm, sm.tile[gstep % kRing], dma, rv, lbase, kvb, row_bytes,
+                              qs[j + 1] - qs[j] - s * kQRows, st, [&] {
+                                if (last && jn < nq) query_load_q(p, bi, m0 + jn, st);
+                              });
     }
     if (ns > 0 && jn < nq) qloaded = jn;
     query_epilogue<kRing>(p, sm, bi * p.m + m0 + j, bi, m0 + j, st);
