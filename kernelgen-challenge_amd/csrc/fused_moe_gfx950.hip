@@ -653,8 +653,9 @@ __global__ void __launch_bounds__(256, 1) fm_gemm_kernel(const GemmParams p) {
 // so a stage moves 128 flop per byte into LDS (85 for the 128-pair tile), and
 // the second wave on each SIMD issues MFMAs while the first waits for its
 // fragment reads. K streams in 32-wide stages through a 4-deep ring (32 KiB
-// per stage: A 256 rows, then B 256 rows, of 64 bytes): three stages are in
-// flight while one is read. Row r's 16-byte chunk c sits at c ^ ((r >> 2) & 3):
+// per stage: A 256 rows, then B 256 rows, of 64 bytes), in pairs: two stages
+// are in flight while the other two are read. Row r's 16-byte chunk c sits at
+// c ^ ((r >> 2) & 3):
 // 16 consecutive rows of one chunk (a fragment read's LDS cycle) then hit 16
 // distinct groups of 4 banks. Each wave moves A rows 32w..32w+31 and B rows
 // 32w..32w+31 of every stage (two 16-row LDS-DMA instructions each; A rows
@@ -685,7 +686,6 @@ __device__ __forceinline__ void big_tile(const GemmParams& p, const uint8_t* s_b
   const int l32 = lane & 31;
   const int hi = lane >> 5;
   const int nst = p.kin / kBigBK;
-  const int per_stage = na + 2;  // this wave's DMAs per stage
   auto issue = [&](int st) {
     const uint32_t sb = lds0 + uint32_t((st % kBigStages) * kBigStage);
     const int64_t k0 = int64_t(st) * kBigRowBytes;
@@ -705,16 +705,18 @@ __device__ __forceinline__ void big_tile(const GemmParams& p, const uint8_t* s_b
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[rb][cb][i] = 0.f;
 
-  for (int st = 0; st < kBigStages - 1 && st < nst; ++st) issue(st);
+  // Stages go in pairs: one wait and barrier per pair. Before pair (st,
+  // st + 1) only its own loads are in flight; after the barrier the next
+  // pair's are issued into the buffers of the pair every wave has just
+  // finished (one barrier per 64 k instead of per 32: 1-7 % faster).
+  static_assert(kBigStages == 4, "two pairs of stage buffers");
+  for (int st = 0; st < 2 && st < nst; ++st) issue(st);
   for (int st = 0; st < nst; ++st) {
-    // this wave's loads of stage st are complete (those of the up to two
-    // stages issued after it may still fly), then every wave's are
-    wait_vmcnt(min(nst - 1, st + kBigStages - 2) - st > 0
-                   ? (min(nst - 1, st + kBigStages - 2) - st) * per_stage
-                   : 0);
-    lds_barrier();
-    // the buffer of stage st - 1, which every wave has finished reading
-    if (st + kBigStages - 1 < nst) issue(st + kBigStages - 1);
+    if ((st & 1) == 0) {
+      wait_vmcnt(0);
+      lds_barrier();
+      for (int s2 = st + 2; s2 < st + 4 && s2 < nst; ++s2) issue(s2);
+    }
     if constexpr (NRB > 0) {
       const uint8_t* sa = s_buf + (st % kBigStages) * kBigStage;
       const uint8_t* sb = sa + kBigAStage;
