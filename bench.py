@@ -434,7 +434,8 @@ def moe_gemm_kernel(M, N, E, topk, gated):
     avg = P / E
     g = "true" if gated else "false"
     if avg > 24.0:
-        big = avg >= 256.0 and (P // 256) * (N // 128) >= 256
+        fills = 128.0 <= avg < 208.0 or avg >= 360.0
+        big = fills and (P // 256) * (N // 128) >= 256
         return f"fm_gemm_big_kernel<{g}>" if big else f"fm_gemm_kernel<{g}>"
     pb = 4 if avg > 24.0 and N % 256 == 0 else 2 if avg > 12.0 else 1
     if N % 256 == 0:

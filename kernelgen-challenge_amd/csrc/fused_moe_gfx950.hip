@@ -79,12 +79,18 @@ Plan make_plan(const fm_args* a) {
     p.large = false;
   else
     p.large = avg > 24.0;
-  // 256-pair tiles once an expert's pairs fill them on average and their
-  // gate-up GEMM still has a work-group for each of MI355X's 256 CUs
-  // (P / 256 pair tiles x N / 128 column tiles); fewer, and the 128-pair
-  // tiles' larger grid is faster (measured at M = 1024, 2048 with E = 8)
+  // 256-pair tiles when an expert's pairs fill them well and their gate-up
+  // GEMM still has a work-group for each of MI355X's 256 CUs (P / 256 pair
+  // tiles x N / 128 column tiles; fewer, and the 128-pair tiles' larger grid
+  // is faster: measured at M = 1024, 2048 with E = 8). Which fills better
+  // depends on the pairs per expert (K = 2048, N = 1024, E = 64, whole
+  // calls): 256-pair tiles win at 136-192 on average (most experts fit one,
+  // 4-8 %) and from 384 on; 128-pair tiles below 130 and at 225-336, where
+  // many experts spill a few pairs into a second, nearly empty 256-pair tile
+  // (2-10 %).
+  const bool fills = (avg >= 128.0 && avg < 208.0) || avg >= 360.0;
   p.big = (a->flags & FM_FLAG_BIG_TILES) != 0 ||
-          ((a->flags & FM_FLAG_LARGE_TILES) == 0 && p.large && avg >= 256.0 &&
+          ((a->flags & FM_FLAG_LARGE_TILES) == 0 && p.large && fills &&
            (p.P / 256) * (a->N / 128) >= 256);
   // 16 or 32 pairs per small tile (64 only when forced; measured slower than
   // the large tiles at 48 pairs per expert)
