@@ -717,40 +717,48 @@ __device__ __forceinline__ void big_tile(const GemmParams& p, const uint8_t* s_b
   // finished (one barrier per 64 k instead of per 32: 1-7 % faster).
   static_assert(kBigStages == 4, "two pairs of stage buffers");
   for (int st = 0; st < 2 && st < nst; ++st) issue(st);
-  for (int st = 0; st < nst; ++st) {
-    if ((st & 1) == 0) {
-      wait_vmcnt(0);
-      lds_barrier();
-      for (int s2 = st + 2; s2 < st + 4 && s2 < nst; ++s2) issue(s2);
-    }
-    if constexpr (NRB > 0) {
-      const uint8_t* sa = s_buf + (st % kBigStages) * kBigStage;
-      const uint8_t* sb = sa + kBigAStage;
-      // both k-steps' fragments first: the second's reads fly under the
-      // first's MFMAs
-      bf16x8 bf[2][2], af[2][NRB];
+  // one stage's fragment reads (both k-steps) and MFMAs
+  auto reads = [&](int st, bf16x8 (&bf)[2][2], bf16x8 (&af)[2][NRB > 0 ? NRB : 1]) {
+    const uint8_t* sa = s_buf + (st % kBigStages) * kBigStage;
+    const uint8_t* sb = sa + kBigAStage;
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int c = 2 * kk + hi;
+    for (int kk = 0; kk < 2; ++kk) {
+      const int c = 2 * kk + hi;
 #pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          const int lr = 64 * wq + 32 * cb + l32;
-          bf[kk][cb] = *reinterpret_cast<const bf16x8*>(sb + lr * kBigRowBytes + swz4(lr, c) * 16);
-        }
-#pragma unroll
-        for (int rb = 0; rb < NRB; ++rb) {
-          const int r = 128 * ph + 32 * rb + l32;
-          af[kk][rb] = *reinterpret_cast<const bf16x8*>(sa + r * kBigRowBytes + swz4(r, c) * 16);
-        }
+      for (int cb = 0; cb < 2; ++cb) {
+        const int lr = 64 * wq + 32 * cb + l32;
+        bf[kk][cb] = *reinterpret_cast<const bf16x8*>(sb + lr * kBigRowBytes + swz4(lr, c) * 16);
       }
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
+      for (int rb = 0; rb < NRB; ++rb) {
+        const int r = 128 * ph + 32 * rb + l32;
+        af[kk][rb] = *reinterpret_cast<const bf16x8*>(sa + r * kBigRowBytes + swz4(r, c) * 16);
+      }
+    }
+  };
+  auto mfmas = [&](const bf16x8 (&bf)[2][2], const bf16x8 (&af)[2][NRB > 0 ? NRB : 1]) {
 #pragma unroll
-        for (int rb = 0; rb < NRB; ++rb)
+    for (int kk = 0; kk < 2; ++kk)
 #pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
-            acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk][rb], bf[kk][cb],
-                                                                   acc[rb][cb], 0, 0, 0);
+      for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+          acc[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk][rb], bf[kk][cb],
+                                                                 acc[rb][cb], 0, 0, 0);
+  };
+  // nst is even: validate() requires K % 256 == 0 and N % 128 == 0
+  for (int st = 0; st < nst; st += 2) {
+    wait_vmcnt(0);
+    lds_barrier();
+    for (int s2 = st + 2; s2 < st + 4 && s2 < nst; ++s2) issue(s2);
+    if constexpr (NRB > 0) {
+      // the pair in one body: the second stage's fragment reads fly under
+      // the first's MFMAs (1-4 % against a loop over single stages)
+      bf16x8 bf0[2][2], af0[2][NRB], bf1[2][2], af1[2][NRB];
+      reads(st, bf0, af0);
+      reads(st + 1, bf1, af1);
+      mfmas(bf0, af0);
+      mfmas(bf1, af1);
     }
   }
 
