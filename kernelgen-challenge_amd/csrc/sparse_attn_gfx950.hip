@@ -584,12 +584,14 @@ __device__ __forceinline__ void query_epilogue(const FwdParams& p, QuerySmemT<kR
 #pragma unroll
     for (int j = 0; j < 4; ++j) fj[j] = __shfl(f, 4 * g + j);
     __bf16* ob = p.o + bi * p.so_b + mi * p.so_m;
+    // o and the partials are written once and not read again by this launch:
+    // nontemporal stores keep them from taking L2 lines from the gathered rows
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       __bf16* orow = ob + int64_t(4 * g + j) * p.so_h + dcol;
 #pragma unroll
       for (int blk = 0; blk < kDBlocks; ++blk)
-        orow[16 * blk] = static_cast<__bf16>(oacc[blk][j] * fj[j]);
+        __builtin_nontemporal_store(static_cast<__bf16>(oacc[blk][j] * fj[j]), &orow[16 * blk]);
     }
   } else {
     float* part = p.part + unit * kPartFloats;
@@ -602,7 +604,7 @@ __device__ __forceinline__ void query_epilogue(const FwdParams& p, QuerySmemT<kR
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int blk = 0; blk < kDBlocks; ++blk)
-        po[(4 * g + j) * kDim + dcol + 16 * blk] = oacc[blk][j];
+        __builtin_nontemporal_store(oacc[blk][j], &po[(4 * g + j) * kDim + dcol + 16 * blk]);
   }
 }
 
@@ -1728,6 +1730,8 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
     }
   }
   lds_barrier();
+  // Nontemporal: the tile's o is not read again by this launch, and its
+  // 128 KiB would otherwise take L2 lines from the other tiles' rows.
   __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + 128 * wave + l32;
 #pragma unroll
   for (int k = 0; k < 4; ++k)
@@ -1742,7 +1746,8 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
           __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t((col0 + b) & 15) * p.so_h;
 #pragma unroll
           for (int db = 0; db < 4; ++db)
-            orow[32 * db] = static_cast<__bf16>(oacc[4 * k + db][4 * a + b] * fs[b]);
+            __builtin_nontemporal_store(static_cast<__bf16>(oacc[4 * k + db][4 * a + b] * fs[b]),
+                                        &orow[32 * db]);
         }
       }
     }
