@@ -1732,22 +1732,35 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
   lds_barrier();
   // Nontemporal: the tile's o is not read again by this launch, and its
   // 128 KiB would otherwise take L2 lines from the other tiles' rows.
-  __bf16* ob = p.o + bi * p.so_b + q0 * p.so_m + 128 * wave + l32;
+  // Column c = 32kk + 8a + 4hi + b is o row (query c / 16, head c % 16): a
+  // per-lane base (hi, d) plus a wave-uniform offset, so the row addresses
+  // are scalar arithmetic. Columns b and b + 1 share one conversion; the
+  // upper half is stored by the d16_hi form.
+  __bf16* const lbase = p.o + bi * p.so_b + q0 * p.so_m + int64_t(4 * hi) * p.so_h + 128 * wave + l32;
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int k = 0; k < 4; ++k)
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      const int col0 = 32 * ((wave + k) & 3) + 8 * a + 4 * hi;  // columns col0 .. col0 + 3
+      const int kk = (wave + k) & 3;
+      const int col0 = 32 * kk + 8 * a + 4 * hi;  // columns col0 .. col0 + 3
       const f32x4 fs = *reinterpret_cast<const f32x4*>(&s_f[col0]);
-      const int q2 = col0 >> 4;
+      const int q2 = 2 * kk + (a >> 1);           // wave-uniform
       if (q2 < qt) {
+        const int64_t uoff = int64_t(q2) * p.so_m + int64_t(8 * (a & 1)) * p.so_h;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          __bf16* orow = ob + int64_t(q2) * p.so_m + int64_t((col0 + b) & 15) * p.so_h;
+        for (int b = 0; b < 4; b += 2) {
+          __bf16* r0 = lbase + uoff + int64_t(b) * p.so_h;
+          __bf16* r1 = r0 + p.so_h;
 #pragma unroll
-          for (int db = 0; db < 4; ++db)
-            __builtin_nontemporal_store(static_cast<__bf16>(oacc[4 * k + db][4 * a + b] * fs[b]),
-                                        &orow[32 * db]);
+          for (int db = 0; db < 4; ++db) {
+            const f32x2_t f2 = {oacc[4 * k + db][4 * a + b] * fs[b],
+                                oacc[4 * k + db][4 * a + b + 1] * fs[b + 1]};
+            const bf16x2_t h2 = __builtin_convertvector(f2, bf16x2_t);
+            __builtin_nontemporal_store(h2[0], &r0[32 * db]);
+            __builtin_nontemporal_store(h2[1], &r1[32 * db]);
+          }
         }
       }
     }
