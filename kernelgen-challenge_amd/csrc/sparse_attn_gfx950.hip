@@ -914,12 +914,17 @@ __device__ __forceinline__ void query_stream(const FwdParams& p, int64_t bi, int
 //  3. write: the waves' run lengths give each its first union entry; a
 //     ballot per chunk ranks the nonzero rows, so the union is written in
 //     ascending row order with consecutive lanes on consecutive entries.
-constexpr int kIdxThreads = 512;
-constexpr int kIdxWaves = kIdxThreads / 64;
-constexpr int kIdxVec = 4;    // index vectors per thread per round
+// 1024 threads with 2 vectors per round from kIdxWideKv rows (the count
+// table then allows one work-group per CU): the 1x16384 kv_len 16384 topk 128
+// shape's index kernel 31.6 -> 26.1 us; 512 threads with 4 vectors below.
+constexpr int kIdxThreadsNarrow = 512;
+constexpr int kIdxVecNarrow = 4;    // index vectors per thread per round
+constexpr int64_t kIdxWideKv = 8192;
 constexpr int kIdxScan = 4;   // LDS chunk reads per wave per batch
 
+template <int kIdxThreads, int kIdxVec>
 __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexParams p) {
+  constexpr int kIdxWaves = kIdxThreads / 64;
   extern __shared__ unsigned long long s_count[];  // [kv_len], byte q = count in query q
   constexpr int kMaxChunks = int(sa::kMaxTileKv / 64);
   __shared__ uint8_t s_cnz[kMaxChunks];    // 64-row chunk holds a named row
@@ -2149,13 +2154,21 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     const bool placed = what == Launch::kCall && !planned && ip.placed_regime != 0;
     if (!planned) {
       const size_t lds = size_t(a->kv_len) * sizeof(unsigned long long);
+      // long caches (one work-group per CU by LDS): twice the threads, half
+      // the index vectors each
+      const bool wide = a->kv_len >= kIdxWideKv;
+      const void* ik = wide ? reinterpret_cast<const void*>(sa_tile_index_kernel<1024, 2>)
+                            : reinterpret_cast<const void*>(sa_tile_index_kernel<kIdxThreadsNarrow, kIdxVecNarrow>);
       if (lds > 65536 &&
-          hipFuncSetAttribute(reinterpret_cast<const void*>(sa_tile_index_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
+          hipFuncSetAttribute(ik, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
         return SA_EHIP;
       if (!mark(SA_KERNEL_INDEX, 0)) return SA_EHIP;
-      hipLaunchKernelGGL(sa_tile_index_kernel, dim3(unsigned(plan.ntiles)), dim3(kIdxThreads),
-                         lds, stream, ip);
+      if (wide)
+        hipLaunchKernelGGL((sa_tile_index_kernel<1024, 2>), dim3(unsigned(plan.ntiles)), dim3(1024),
+                           lds, stream, ip);
+      else
+        hipLaunchKernelGGL((sa_tile_index_kernel<kIdxThreadsNarrow, kIdxVecNarrow>),
+                           dim3(unsigned(plan.ntiles)), dim3(kIdxThreadsNarrow), lds, stream, ip);
       if (hipGetLastError() != hipSuccess) return SA_EHIP;
       if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
     }
