@@ -473,11 +473,13 @@ def moe_kernel_times(sets, topk, steps, warmup):
         sa_capi.fm_check(lib, lib.fm_forward(ctypes.byref(args[i % len(args)]),
                                              ctypes.c_void_p(stream.cuda_stream)))
     torch.cuda.synchronize()
+    mask = 0
     for i in range(steps):
-        sa_capi.fm_forward_events(lib, args[i % len(args)], stream.cuda_stream, evs[i])
+        mask = sa_capi.fm_forward_events(lib, args[i % len(args)], stream.cuda_stream, evs[i])
     torch.cuda.synchronize()
+    # kernels the call launches (no final-sum launch for topk <= 2 decode tiles)
     return {name: sum(evs[i][2 * k].elapsed_time(evs[i][2 * k + 1]) for i in range(steps)) / steps
-            for k, name in enumerate(sa_capi.FM_KERNELS)}
+            for k, name in enumerate(sa_capi.FM_KERNELS) if (mask >> k) & 1}
 
 
 def moe_cpu_baseline(hidden, w1, w2, score, topk, target_s=3.0, runs=3):

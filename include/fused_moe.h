@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FM_ABI_VERSION 2
+#define FM_ABI_VERSION 3
 
 enum {
   FM_OK = 0,
@@ -84,7 +84,10 @@ enum {
   FM_KERNEL_PLAN = 1,    /* pairs sorted by expert, tile table       */
   FM_KERNEL_GATEUP = 2,  /* x = h . w1^T, u = up * silu(gate)        */
   FM_KERNEL_DOWN = 3,    /* y = u . w2^T, times the routing weight   */
-  FM_KERNEL_REDUCE = 4,  /* ascending-expert bf16 sum per token      */
+  FM_KERNEL_REDUCE = 4,  /* ascending-expert bf16 sum per token; since
+                            version 3 not launched for topk <= 2 with
+                            streamed (decode) tiles: the down GEMM adds
+                            into out itself                          */
   FM_KERNEL_COUNT = 5
 };
 

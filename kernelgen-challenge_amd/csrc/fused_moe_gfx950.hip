@@ -31,7 +31,10 @@
 //   and the 4 waves of a work-group split K and add their partial sums
 //   through LDS. 16x16x32 bf16 MFMA.
 // fm_reduce_kernel  out[t] = bf16 running sum of the token's topk weighted
-//   expert outputs, ascending expert order.
+//   expert outputs, ascending expert order. Not launched when topk <= 2 and
+//   the tiles are streamed (decode): the routing launch clears out, and the
+//   down GEMM adds each weighted row into it with packed bf16 atomics (the
+//   two-term bf16 sum does not depend on the order).
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -238,7 +241,20 @@ struct RouteParams {
   float* wts;       // [M, topk] bf16-rounded weights (as fp32)
   int64_t M;
   int E, topk, renormalize;
+  // when the down GEMM adds into the output itself: the rows to clear
+  __bf16* zero_out;
+  int64_t s_out;
+  int K;
 };
+
+// Clears output row t (K bf16, 16-byte aligned) by one wave.
+__device__ __forceinline__ void clear_out_row(const RouteParams& p, int64_t t, int lane) {
+  __bf16* row = p.zero_out + t * p.s_out;
+  bf16x8 z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z[e] = static_cast<__bf16>(0.f);
+  for (int k = 8 * lane; k < p.K; k += 8 * 64) *reinterpret_cast<bf16x8*>(row + k) = z;
+}
 
 // Routing of token t by one wave; lane l holds experts l, l + 64, l + 128,
 // l + 192. `raw` are the token's scores as loaded (bf16 widened; -inf past E).
@@ -318,6 +334,7 @@ __global__ void __launch_bounds__(256) fm_route_kernel(const RouteParams p) {
   float raw[kPer];
   load_scores(p, t, lane, raw);
   route_token(p, t, lane, raw);
+  if (p.zero_out != nullptr) clear_out_row(p, t, lane);
 }
 
 // ============================================================================
@@ -424,7 +441,10 @@ __global__ void __launch_bounds__(1024) fm_route_plan_kernel(const RouteParams r
 #pragma unroll
   for (int j = 0; j < kPerWave; ++j) {
     const int64_t t = wave + 16 * j;
-    if (t < rp.M) route_token(rp, t, lane, raw[j]);
+    if (t < rp.M) {
+      route_token(rp, t, lane, raw[j]);
+      if (rp.zero_out != nullptr) clear_out_row(rp, t, lane);
+    }
   }
   // the ids and weights are in memory before any thread of the group reads
   // them back (same CU: the workgroup barrier orders them once stored)
@@ -456,7 +476,22 @@ struct GemmParams {
   int topk;
   int col_tiles;         // output-column tiles per pair tile
   int ct_per_wg;         // column tiles one work-group runs (fm_stream_kernel)
+  // GEMM 2 with topk <= 2 (fm_stream_kernel): add each pair's bf16 row into
+  // the token's output row instead of writing yw (null: write yw)
+  __bf16* fsum;
+  int64_t fsum_stride;
 };
+
+// out[0..1] += (a0, a1) as one packed bf16 atomic add at agent scope (sc1:
+// performed where every XCD sees it; the two addends of an element may come
+// from work-groups on different XCDs). Each element gets at most two addends
+// onto the cleared 0, so the result is bf16(x + y): the reference's ascending
+// running sum, whose two-term form does not depend on the order.
+__device__ __forceinline__ void add_bf16x2(__bf16* out, __bf16 a0, __bf16 a1) {
+  const uint32_t v = uint32_t(__builtin_bit_cast(uint16_t, a0)) |
+                     uint32_t(__builtin_bit_cast(uint16_t, a1)) << 16;
+  asm volatile("global_atomic_pk_add_bf16 %0, %1, off sc1" : : "v"(out), "v"(v) : "memory");
+}
 
 // ---- large tiles -------------------------------------------------------------
 // LDS stage: A 128 rows x 128 B, then B 256 rows x 128 B. Row r's 16-byte
@@ -1160,8 +1195,14 @@ __global__ void __launch_bounds__(256, 1) fm_stream_kernel(const GemmParams p) {
           bf16x4 o;
 #pragma unroll
           for (int i = 0; i < 4; ++i) o[i] = static_cast<__bf16>(bf16r(sum[i]) * wt);
-          *reinterpret_cast<bf16x4*>(p.out + int64_t(pair) * p.out_stride + 32 * ct + 16 * b +
-                                     4 * lg) = o;
+          if (p.fsum != nullptr) {
+            __bf16* fo = p.fsum + int64_t(pair / p.topk) * p.fsum_stride + 32 * ct + 16 * b + 4 * lg;
+            add_bf16x2(fo, o[0], o[1]);
+            add_bf16x2(fo + 2, o[2], o[3]);
+          } else {
+            *reinterpret_cast<bf16x4*>(p.out + int64_t(pair) * p.out_stride + 32 * ct + 16 * b +
+                                       4 * lg) = o;
+          }
         }
       }
     }
@@ -1234,6 +1275,16 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   rp.E = int(a->E);
   rp.topk = int(a->topk);
   rp.renormalize = a->renormalize ? 1 : 0;
+  // With at most two experts per token, the down GEMM of streamed tiles adds
+  // into the output itself and the routing launch clears it: no final-sum
+  // launch.
+  const bool streamed = !pl.large && a->N % kStK == 0;  // (K % 256 == 0 always holds)
+  const bool fsum = streamed && a->topk <= 2;
+  if (fsum) {
+    rp.zero_out = static_cast<__bf16*>(a->out);
+    rp.s_out = a->s_out;
+    rp.K = int(a->K);
+  }
   PlanParams pp{};
   pp.ids = ids;
   pp.eoff = eoff;
@@ -1287,7 +1338,10 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   }
   // small tiles stream their weights through LDS when both reductions are
   // whole 256-wide stages, else straight into registers
-  const bool streamed = !pl.large && a->N % kStK == 0;  // (K % 256 == 0 always holds)
+  if (fsum) {
+    g2.fsum = static_cast<__bf16*>(a->out);
+    g2.fsum_stride = a->s_out;
+  }
   g1.ct_per_wg = g2.ct_per_wg = 1;
   if (streamed) {
     // a streaming work-group runs several column tiles in one pipeline, so its
@@ -1337,6 +1391,7 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
     hipLaunchKernelGGL((fm_skinny_kernel<false, 2>), dim3(grid2), dim3(256), 0, stream, g2);
   if (!launched_ok(FM_KERNEL_DOWN)) return FM_EHIP;
 
+  if (fsum) return FM_OK;
   ReduceParams rd{};
   rd.yw = yw;
   rd.out = static_cast<__bf16*>(a->out);

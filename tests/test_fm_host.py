@@ -45,7 +45,7 @@ def test_exports_every_declared_function(lib):
                           "fm_workspace_bytes"]
     for name in declared():
         assert hasattr(lib, name)
-    assert lib.fm_abi_version() == 2
+    assert lib.fm_abi_version() == 3
 
 
 def test_binding_matches_header_struct():

@@ -208,7 +208,7 @@ def test_capi_matches_operator_and_times_kernels(gpu_sa, shape, flags):
     hidden, w1, w2, score = make_inputs(M, K, N, E, seed=10)
     ref = op(hidden, w1, w2, score, topk, flags=flags)
     lib = sa_capi.fm_load()
-    assert lib.fm_abi_version() == 2
+    assert lib.fm_abi_version() == 3
     out = torch.full_like(hidden, float("nan"))
     a = sa_capi.fm_make_args(hidden, w1, w2, score, out, topk, flags=flags)
     n = sa_capi.fm_workspace_bytes(lib, a)
@@ -222,9 +222,15 @@ def test_capi_matches_operator_and_times_kernels(gpu_sa, shape, flags):
     mask = sa_capi.fm_forward_events(lib, a, stream.cuda_stream, evs)
     torch.cuda.synchronize()
     every = (1 << sa_capi.FM_KERNEL_COUNT) - 1
-    # up to 16 tokens, routing and plan are one launch (reported as the plan)
+    # up to 16 tokens, routing and plan are one launch (reported as the plan);
+    # with topk <= 2 and streamed tiles (at most 24 pairs per expert) the down
+    # GEMM adds into the output and there is no final-sum launch
     route = 1 << sa_capi.FM_KERNELS.index("route")
-    assert mask == (every & ~route if M <= 16 else every)
+    reduce = 1 << sa_capi.FM_KERNELS.index("reduce")
+    expect = every & ~route if M <= 16 else every
+    if topk <= 2 and M * topk / E <= 24 and N % 256 == 0:
+        expect &= ~reduce
+    assert mask == expect
     assert torch.equal(out, ref)
     for k in range(sa_capi.FM_KERNEL_COUNT):
         if (mask >> k) & 1:
