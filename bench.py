@@ -71,7 +71,7 @@ PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 H, D = wl.NUM_HEADS, wl.HEAD_DIM
 KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel",
                 "tile": "sa_fwd_tile_kernel", "query": "sa_fwd_query_kernel",
-                "combine": "sa_combine_kernel"}
+                "combine": "sa_combine_kernel", "wave": "sa_fwd_wave_kernel"}
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the same
@@ -157,9 +157,10 @@ def kernel_times(sets, scale, steps, warmup):
     """Average launch duration (ms) of each kernel over `steps` calls, from
     the HIP events sa_forward_events records on the calls' stream, and each
     kernel's share of the valid slots. In a shared-row plan the tile kernel
-    runs the shared tiles' slots and the per-query kernel the others: the
-    tile meta the index kernel leaves at workspace offset 0 (per tile: union
-    size, mode, valid slots, overflow) tells them apart."""
+    runs the shared tiles' slots and the per-query (or wave) kernel the
+    others: the tile meta the index kernel leaves at workspace offset 0 (per
+    tile: union size, mode, valid slots, overflow) tells them apart. Next to
+    the wave kernel the per-query launch only makes the tile order."""
     import sa_capi
     lib = sa_capi.load()
     stream = torch.cuda.current_stream()
@@ -187,15 +188,17 @@ def kernel_times(sets, scale, steps, warmup):
              if (masks[i] >> k) & 1]
         if d:
             times[name] = sum(d) / len(d)
-    shares = {"query": 1.0, "combine": 1.0}
+    shares = {"query": 1.0, "combine": 1.0, "wave": 1.0}
     if masks[-1] & (1 << sa_capi.KERNELS.index("index")):
         b, m = sets[0][0].shape[:2]
         ntiles = b * -(-m // 8)
         meta = ws[:16 * ntiles].view(torch.int32).view(ntiles, 4).cpu().long()
         total = int(meta[:, 2].sum())
         shared = int(meta[meta[:, 1] == 1, 2].sum())
+        per_query = (total - shared) / total if total else 0.0
+        wave = (masks[-1] >> sa_capi.KERNELS.index("wave")) & 1
         shares = {"tile": shared / total if total else 1.0,
-                  "query": (total - shared) / total if total else 0.0}
+                  "query": 0.0 if wave else per_query, "wave": per_query}
     return times, shares
 
 

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 5
+#define SA_ABI_VERSION 6
 
 /* Return codes. */
 enum {
@@ -204,7 +204,11 @@ int sa_forward_noalloc(const sa_args* a, void* hip_stream);
  * QUERY, TILE. In a tile plan the QUERY launch runs the queries of the tiles
  * the index kernel made per query, and makes the longest-first tile order
  * in its first work-group. (Version 5: the order no longer has a launch of
- * its own, so bit SA_KERNEL_ORDER is never set.)
+ * its own, so bit SA_KERNEL_ORDER is never set.) Version 6: unsplit plans
+ * with topk <= 640 run their per-query
+ * queries as WAVE instead, one wave per query; in a tile plan that makes
+ * the tile order needs, QUERY is then a one-work-group launch that only
+ * makes it.
  */
 enum {
   SA_KERNEL_INDEX = 0,    /* row unions of shared-row tiles (tile plans)   */
@@ -213,7 +217,8 @@ enum {
   SA_KERNEL_QUERY = 3,    /* per-query parts; in tile plans the per-query
                              tiles and the tile order                      */
   SA_KERNEL_COMBINE = 4,  /* merge of split-topk parts (split plans)       */
-  SA_KERNEL_COUNT = 5
+  SA_KERNEL_WAVE = 5,     /* short unsplit queries, one wave per query     */
+  SA_KERNEL_COUNT = 6
 };
 
 /*

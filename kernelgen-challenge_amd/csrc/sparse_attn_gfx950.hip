@@ -261,6 +261,15 @@ __device__ __forceinline__ void mfma_agpr(f32x16& c, bf16x8 a, bf16x8 b) {
       : "v"(a), "v"(b));
 }
 
+// v_mfma_f32_16x16x16_bf16 accumulating in AGPRs (the same hazards).
+__device__ __forceinline__ void mfma16_agpr(f32x4& c, bf16x4 a, bf16x4 b) {
+  asm volatile(
+      "s_nop 1\n\t"
+      "v_mfma_f32_16x16x16_bf16 %0, %1, %2, %0"
+      : "+a"(c)
+      : "v"(a), "v"(b));
+}
+
 __device__ __forceinline__ void mfma_agpr_drain() {
   asm volatile("s_nop 7\n\ts_nop 7" ::: "memory");
 }
@@ -1350,6 +1359,323 @@ __global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
 }
 
 // ============================================================================
+// per-query wave launch
+// ============================================================================
+// For short queries (topk <= kWaveMaxTopk, no split): one wave64 work-group
+// per kWQueries consecutive queries (of a per-query tile in a shared-row
+// plan, else of the flattened b x m), run as
+// one stream of kWRows-row steps through the wave's own 2-deep LDS ring, with
+// no barrier and no exchange with another wave. Per step:
+//  * S^T = K . Q^T with v_mfma_f32_16x16x32_bf16 (16 rows x 16 heads, K = d,
+//    Q^T resident in registers); the 16 gathers of the next step ride between
+//    its 16 MFMAs;
+//  * the online softmax of the 16 heads inside the wave (a head's 16 scores
+//    sit in 4 lanes x 4 values);
+//  * O += P . V with v_mfma_f32_16x16x16_bf16. The S^T accumulator layout
+//    (lane (head n, g) holds rows 4g..4g+3) is that MFMA's A operand layout,
+//    so P stays in registers; V comes from the same LDS rows by transposing
+//    reads.
+// Four work-groups fit in a CU's LDS, one per SIMD, and a CU takes the next
+// one as soon as one ends, so one wave's start and end overlap the others'
+// steps. The list holds 32-bit byte offsets of the rows in the query's batch
+// of kv (the host checks that they fit).
+constexpr int kWRows = 16;               // rows per step
+constexpr int kWPitch = kRowBytes + 48;  // LDS row pitch (bytes)
+constexpr int kWQueries = 2;             // queries per work-group
+constexpr int kWaveMaxTopk = 640;        // slots per query the list holds
+constexpr int kWSlots = kWaveMaxTopk / 64;
+static_assert(kTQ % kWQueries == 0, "a tile's queries split evenly");
+static_assert(kWQueries == 2, "the cursor state is two queries' scalars");
+static_assert(kDim / 32 == kWRows, "one gather per S^T MFMA");
+
+struct WaveSmem {
+  uint8_t tile[2][kWRows * kWPitch];
+  int32_t list[kWQueries * kWaveMaxTopk];
+};
+static_assert(4 * sizeof(WaveSmem) <= 160 * 1024, "four work-groups per CU");
+
+// Stores query (bi, mi)'s o (and lse) from the wave's state: lane (n, g)
+// holds O[head 4g + j][16 blk + n]. Lanes n and n ^ 1 swap half their values
+// (DPP), so that each store writes two adjacent columns of one head: the even
+// lane heads 4g and 4g + 1, the odd lane heads 4g + 2 and 4g + 3. Needs o and
+// its strides 4-byte aligned (validate() asks for 16 bytes).
+__device__ __forceinline__ void wave_epilogue(const FwdParams& p, int64_t bi, int64_t mi,
+                                              float m_run, float l_run, const f32x4 (&oacc)[32]) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  const int lane = threadIdx.x & 63;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  const float lt = wave_sum16(l_run);
+  float lse;
+  const float f = sink_fold(m_run, lt, p.sink[n] * kLog2e, lse);
+  if (p.lse != nullptr && g == 0) p.lse[bi * p.sl_b + mi * p.sl_m + int64_t(n) * p.sl_h] = lse;
+  float fj[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) fj[j] = __shfl(f, 4 * g + j);
+  const bool odd = (n & 1) != 0;
+  __bf16* const r0 =
+      p.o + bi * p.so_b + mi * p.so_m + int64_t(4 * g + (odd ? 2 : 0)) * p.so_h + (n & ~1);
+  __bf16* const r1 = r0 + p.so_h;
+  auto swap = [](float x) {  // the value of lane n ^ 1
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0xB1, 0xF, 0xF, false));
+  };
+#pragma unroll
+  for (int blk = 0; blk < 32; ++blk) {
+    const float v0 = oacc[blk][0] * fj[0], v1 = oacc[blk][1] * fj[1];
+    const float v2 = oacc[blk][2] * fj[2], v3 = oacc[blk][3] * fj[3];
+    const float x0 = swap(odd ? v0 : v2);
+    const float x1 = swap(odd ? v1 : v3);
+    const f32x2 a = odd ? f32x2{x0, v2} : f32x2{v0, x0};
+    const f32x2 b = odd ? f32x2{x1, v3} : f32x2{v1, x1};
+    const bf16x2 ha = __builtin_convertvector(a, bf16x2);
+    const bf16x2 hb = __builtin_convertvector(b, bf16x2);
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, ha),
+                                reinterpret_cast<uint32_t*>(r0 + 16 * blk));
+    __builtin_nontemporal_store(__builtin_bit_cast(uint32_t, hb),
+                                reinterpret_cast<uint32_t*>(r1 + 16 * blk));
+  }
+}
+
+// In a shared-row plan (FwdParams::meta set) work-group i runs queries
+// kWQueries * (i % parts) .. of tile i / parts (parts = kTQ / kWQueries) when
+// the index kernel made that tile per query; else queries kWQueries * i .. of
+// the p.nblocks queries of b x m (two of them may be in different batches).
+__global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
+  __shared__ __attribute__((aligned(16))) WaveSmem sm;
+  constexpr int kParts = kTQ / kWQueries;
+  const int lane = threadIdx.x;
+  const int n = lane & 15;
+  const int g = lane >> 4;
+  int64_t q0;  // the first query, as b * m + m
+  int nq;
+  if (p.meta != nullptr) {
+    const int64_t t = blockIdx.x / kParts;
+    const int64_t m0 = (t % p.tiles_per_b) * kTQ + (blockIdx.x % kParts) * kWQueries;
+    if (__builtin_amdgcn_readfirstlane(p.meta[t * kMetaInts + 1]) == kModeShared) return;
+    nq = int(min(int64_t(kWQueries), p.m - m0));
+    q0 = (t / p.tiles_per_b) * p.m + m0;
+  } else {
+    q0 = int64_t(blockIdx.x) * kWQueries;
+    nq = int(min(int64_t(kWQueries), p.nblocks - q0));
+  }
+  if (nq <= 0) return;
+  // batch and query of the two queries, as scalars (small arrays indexed by a
+  // loop variable end up in LDS, and what is read from there is not known
+  // to be uniform)
+  const int64_t qb0 = q0 / p.m, qm0 = q0 - qb0 * p.m;
+  const int64_t q1 = q0 + (nq > 1 ? 1 : 0);
+  const int64_t qb1 = q1 / p.m, qm1 = q1 - qb1 * p.m;
+  auto qb_of = [&](int j) { return j == 0 ? qb0 : qb1; };
+  auto qm_of = [&](int j) { return j == 0 ? qm0 : qm1; };
+  auto kv_of = [&](int j) {
+    return reinterpret_cast<const uint8_t*>(p.kv + qb_of(j) * p.skv_b);
+  };
+  const int topk = int(p.topk);
+  const uint32_t row_bytes = uint32_t(p.skv_n * 2);
+
+  // ---- indices, then query 0's Q^T (B operand: lane (n, g) holds head n,
+  // d = 32s + 8g .. +7 for k-step s) ----------------------------------------------
+  int raw[kWQueries][kWSlots];
+#pragma unroll
+  for (int j = 0; j < kWQueries; ++j)
+#pragma unroll
+    for (int i = 0; i < kWSlots; ++i) {
+      const int sl = 64 * i + lane;
+      raw[j][i] = (j < nq && sl < topk) ? p.idx[qb_of(j) * p.si_b + qm_of(j) * p.si_m + sl] : -1;
+    }
+  bf16x8 qf[kDim / 32];
+  auto load_q = [&](int j) {
+    const __bf16* qrow =
+        p.q + qb_of(j) * p.sq_b + qm_of(j) * p.sq_m + int64_t(n) * p.sq_h + 8 * g;
+#pragma unroll
+    for (int s = 0; s < kDim / 32; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
+  };
+  load_q(0);
+
+  // ---- compaction: query j's valid slots at list[qsel(j) .. qsel(j + 1)) ----------
+  const unsigned long long below = (1ull << lane) - 1ull;
+  int pos = 0, qs1 = 0;
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < kWQueries; ++j) {
+    if (j == 1) qs1 = pos;
+#pragma unroll
+    for (int i = 0; i < kWSlots; ++i) {
+      const int v = raw[j][i];
+      const bool ok = (v >= 0) && (int64_t(v) < p.kv_len);
+      bad |= (!ok && v != -1);
+      const unsigned long long bm = __ballot(ok);
+      if (ok) sm.list[pos + __popcll(bm & below)] = int32_t(uint32_t(v) * row_bytes);
+      pos += __popcll(bm);
+    }
+  }
+  const int qs2 = pos;
+  if (bad && p.err != nullptr) flag_bad_index(p.err);
+  __syncthreads();  // the list is written before it is read
+  auto qsel = [&](int j) { return j <= 0 ? 0 : j == 1 ? qs1 : qs2; };
+  auto nst = [&](int j) { return (qsel(j + 1) - qsel(j) + kWRows - 1) / kWRows; };
+  int total = 0;
+#pragma unroll
+  for (int j = 0; j < kWQueries; ++j) total += nst(j);
+  // Q^T and the indices complete before the first gather is issued, so that
+  // every later vmcnt(0) waits for the ring (and a Q^T issued after a gather)
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+
+  // ---- the step stream ------------------------------------------------------------
+  // The issue cursor (ji, si): query and step of the next step to gather. Lane
+  // n < 16 holds the entry of the step's row n; entries past a query's last
+  // valid one take its first entry's row, whose scores are masked.
+  const uint32_t lds_rows = __builtin_amdgcn_readfirstlane(
+      uint32_t(reinterpret_cast<uintptr_t>((lds_u8_t*)&sm.tile[0][0])));
+  int ji = 0, si = 0;
+  while (ji < kWQueries && nst(ji) == 0) ++ji;
+  // the rows' entries for the cursor's step; kvg = the base of their batch
+  const uint8_t* kvg = nullptr;
+  auto cursor_rows = [&]() {
+    const int e0 = qsel(ji);
+    const int e = e0 + si * kWRows + n;
+    const int rv = sm.list[e < qsel(ji + 1) ? e : e0];
+    kvg = kv_of(ji);
+    if (++si == nst(ji)) {
+      si = 0;
+      do {
+        ++ji;
+      } while (ji < kWQueries && nst(ji) == 0);
+    }
+    return rv;
+  };
+  // kvg as a scalar (for the gathers' scalar base). readfirstlane returns
+  // int: each half goes through uint32_t so the low one is not sign-extended.
+  auto kv_scalar = [&]() {
+    const uint64_t a = reinterpret_cast<uint64_t>(kvg);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a))));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(a >> 32))));
+    return reinterpret_cast<const uint8_t*>(uint64_t(lo) | uint64_t(hi) << 32);
+  };
+  if (total > 0) {
+    const int rv = cursor_rows();
+    const uint8_t* kvs = kv_scalar();
+#pragma unroll
+    for (int i = 0; i < kWRows; ++i) {
+      const uint32_t off = uint32_t(__builtin_amdgcn_readlane(rv, i));
+      lds_dma_row(kvs + off, 16 * lane, lds_rows + uint32_t(i * kWPitch));
+    }
+  }
+
+  f32x4 oacc[32];
+  float m_run = -INFINITY, l_run = 0.f;
+#pragma unroll
+  for (int blk = 0; blk < 32; ++blk) oacc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int gstep = 0;
+  int qloaded = 0;  // the query whose Q^T is in qf
+  for (int j = 0; j < nq; ++j) {
+    const int ns = nst(j);
+    int jn = j + 1;  // the next query with a valid slot
+    while (jn < nq && nst(jn) == 0) ++jn;
+    if (ns > 0 && qloaded != j) {  // only after a query without a valid slot
+      load_q(j);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      qloaded = j;
+    }
+    for (int s = 0; s < ns; ++s, ++gstep) {
+      // this step's rows (and a Q^T issued during the last step) have landed,
+      // and the reads of the buffer the next gathers fill are complete
+      __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
+      asm volatile("" ::: "memory");
+      const bool dma = gstep + 1 < total;
+      const int rv = dma ? cursor_rows() : 0;
+      const uint8_t* kvs = kv_scalar();
+      const uint32_t lnext = lds_rows + uint32_t(((gstep + 1) & 1) * kWRows * kWPitch);
+      const uint8_t* tb = sm.tile[gstep & 1];
+      const int nrows = qsel(j + 1) - qsel(j) - s * kWRows;
+
+      // S^T for the step's 16 rows (A: lane (row n, g) reads d = 32s + 8g ..);
+      // two accumulator chains, K fragments read 3 MFMAs ahead
+      f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
+      const uint8_t* krow = tb + n * kWPitch + 16 * g;
+      auto s_chain = [&](auto with_dma) {
+        bf16x8 kf[4];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) kf[k] = *reinterpret_cast<const bf16x8*>(krow + 64 * k);
+#pragma unroll
+        for (int k = 0; k < kDim / 32; ++k) {
+          if (k + 3 < kDim / 32)
+            kf[(k + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (k + 3));
+          if (k & 1)
+            sb = mfma_16x16x32(kf[k & 3], qf[k], sb);
+          else
+            sa = mfma_16x16x32(kf[k & 3], qf[k], sa);
+          if constexpr (decltype(with_dma)::value) {
+            const uint32_t off = uint32_t(__builtin_amdgcn_readlane(rv, k));
+            lds_dma_row(kvs + off, 16 * lane, lnext + uint32_t(k * kWPitch));
+          }
+          __builtin_amdgcn_sched_barrier(0);  // keep the interleave
+        }
+      };
+      if (dma)
+        s_chain(std::true_type{});
+      else
+        s_chain(std::false_type{});
+      if (s == ns - 1 && jn < nq) load_q(jn);  // Q^T is no longer read
+
+      // online softmax: lane (n, g) holds S[head n][row 4g + j]
+      float sv[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        sv[k] = (4 * g + k < nrows) ? (sa[k] + sb[k]) * p.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sv[k]);
+      }
+      mx = wave_max16(mx);  // finite: the step's row 0 is valid
+      float alpha = 1.f;
+      if (mx > m_run + kRescaleLog2) {
+        alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mx);  // O, l still 0 at first
+        m_run = mx;
+      }
+      float psum = 0.f;
+      bf16x4 pb;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float pk = exp2f(sv[k] - m_run);
+        psum += pk;
+        pb[k] = static_cast<__bf16>(pk);
+      }
+      l_run = l_run * alpha + psum;
+      if (__any(alpha != 1.f)) {
+        float ak[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ak[k] = __shfl(alpha, 4 * g + k);
+#pragma unroll
+        for (int blk = 0; blk < 32; ++blk)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) oacc[blk][k] *= ak[k];
+      }
+
+      // O += P . V: lane (n, g) reads V[rows 4g .. 4g + 3][16 blk + n]; O in
+      // AGPRs, the V fragments of 16 column blocks read ahead of their MFMAs
+      const uint8_t* vb = tb + (4 * g + (n >> 2)) * kWPitch + 8 * (n & 3);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        bf16x4 vf[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) vf[i] = lds_read_tr16(vb + 32 * (16 * h + i));
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mfma16_agpr(oacc[16 * h + i], pb, vf[i]);
+      }
+    }
+    if (ns > 0 && jn < nq) qloaded = jn;
+    mfma_agpr_drain();
+    wave_epilogue(p, qb_of(j), qm_of(j), m_run, l_run, oacc);
+    m_run = -INFINITY;
+    l_run = 0.f;
+#pragma unroll
+    for (int blk = 0; blk < 32; ++blk) oacc[blk] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
+// ============================================================================
 // shared-row tile kernel
 // ============================================================================
 // LDS row layout: a gathered row is 1 KiB stored at a 1072-byte pitch, and
@@ -2103,9 +2429,23 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
   p.split_len = plan.split_len;
   p.nblocks = plan.units * plan.nsplit;
 
+  // Short unsplit queries run one wave each (sa_fwd_wave_kernel): its list
+  // holds 32-bit row offsets in a batch of kv. (Its epilogue's bf16 pair
+  // stores need o 4-byte aligned: validate() asks for 16.)
+  const bool wave_ok =
+      what == Launch::kCall && plan.nsplit == 1 && a->topk <= kWaveMaxTopk && a->kv_len > 0 &&
+      (a->kv_len - 1) * a->skv[1] * 2 + 2 * kDim <= int64_t(UINT32_MAX);
+
   // The per-query kernel; two work-groups per CU once there are at least two
   // per CU to run.
   auto launch_query = [&]() -> int {
+    if (p.meta == nullptr && wave_ok) {
+      if (!mark(SA_KERNEL_WAVE, 0)) return SA_EHIP;
+      hipLaunchKernelGGL(sa_fwd_wave_kernel, dim3(unsigned((p.nblocks + kWQueries - 1) / kWQueries)),
+                         dim3(64), 0, stream, p);
+      if (hipGetLastError() != hipSuccess) return SA_EHIP;
+      return mark(SA_KERNEL_WAVE, 1) ? SA_OK : SA_EHIP;
+    }
     if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
     const dim3 grid(unsigned(p.nblocks)), block(kThreads);
     const bool two = p.nblocks >= 2 * int64_t(cus);
@@ -2186,9 +2526,28 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
       p.ord.ntiles = int(plan.ntiles);
       p.ord.cus = cus;
     }
-    p.nblocks = what == Launch::kPlanOnly ? 1 : plan.ntiles + (p.ord.order != nullptr ? 1 : 0);
-    const int lrc = launch_query();
-    if (lrc != SA_OK || what == Launch::kPlanOnly) return lrc;
+    // Short queries run per query as one wave each (sa_fwd_wave_kernel); the
+    // tile order, when this call makes one, is then made by a one-work-group
+    // per-query launch before it.
+    if (wave_ok) {
+      if (p.ord.order != nullptr) {
+        p.nblocks = 1;
+        if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
+        hipLaunchKernelGGL((sa_fwd_query_kernel<2, true>), dim3(1), dim3(kThreads), 0, stream, p);
+        if (hipGetLastError() != hipSuccess) return SA_EHIP;
+        if (!mark(SA_KERNEL_QUERY, 1)) return SA_EHIP;
+        p.ord.order = nullptr;
+      }
+      if (!mark(SA_KERNEL_WAVE, 0)) return SA_EHIP;
+      hipLaunchKernelGGL(sa_fwd_wave_kernel, dim3(unsigned(plan.ntiles * (kTQ / kWQueries))),
+                         dim3(64), 0, stream, p);
+      if (hipGetLastError() != hipSuccess) return SA_EHIP;
+      if (!mark(SA_KERNEL_WAVE, 1)) return SA_EHIP;
+    } else {
+      p.nblocks = what == Launch::kPlanOnly ? 1 : plan.ntiles + (p.ord.order != nullptr ? 1 : 0);
+      const int lrc = launch_query();
+      if (lrc != SA_OK || what == Launch::kPlanOnly) return lrc;
+    }
 
     TileParams tp{};
     tp.q = p.q;

@@ -11,7 +11,7 @@ import sa_capi
 
 pytestmark = pytest.mark.gpu
 
-TILE, QUERY, INDEX, ORDER, COMBINE = 1 << 2, 1 << 3, 1 << 0, 1 << 1, 1 << 4
+TILE, QUERY, INDEX, ORDER, COMBINE, WAVE = 1 << 2, 1 << 3, 1 << 0, 1 << 1, 1 << 4, 1 << 5
 
 
 def case(b, m, kv_len, topk, seed):
@@ -24,9 +24,10 @@ def case(b, m, kv_len, topk, seed):
 
 
 @pytest.mark.parametrize("shape,expect", [
-    ((1, 64, 300, 64), INDEX | QUERY | TILE),           # shared-row plan (order in QUERY)
+    ((1, 64, 300, 64), INDEX | QUERY | WAVE | TILE),    # shared-row plan (order in QUERY)
+    ((1, 300, 2048, 700), INDEX | QUERY | TILE),        # topk above the wave kernel's
     ((4, 1, 2048, 512), QUERY | COMBINE),               # split-topk plan
-    ((1, 3, 2048, 64), QUERY),                          # per query, no split
+    ((1, 3, 2048, 64), WAVE),                           # per query, no split
 ])
 def test_events_hook_matches_operator(gpu_sa, shape, expect):
     q, kv, sink, idx, sc = case(*shape, seed=sum(shape))

@@ -14,7 +14,7 @@ import sa_workloads as wl
 
 pytestmark = pytest.mark.gpu
 
-TILE, QUERY, INDEX, ORDER, COMBINE = 1 << 2, 1 << 3, 1 << 0, 1 << 1, 1 << 4
+TILE, QUERY, INDEX, ORDER, COMBINE, WAVE = 1 << 2, 1 << 3, 1 << 0, 1 << 1, 1 << 4, 1 << 5
 
 
 def case(b, m, kv_len, topk, seed, minus1=0.0):
@@ -119,9 +119,12 @@ def test_plan_of_an_aborting_tile(gpu_sa):
 
 
 @pytest.mark.parametrize("shape,plain,planned", [
-    ((1, 64, 300, 64), INDEX | QUERY | TILE, QUERY | TILE),
+    # short queries: one wave each; the plain call's QUERY launch makes the
+    # tile order, which a planned call already has
+    ((1, 64, 300, 64), INDEX | QUERY | WAVE | TILE, WAVE | TILE),
+    ((1, 300, 2048, 700), INDEX | QUERY | TILE, QUERY | TILE),
     ((4, 1, 2048, 512), QUERY | COMBINE, QUERY | COMBINE),
-    ((1, 3, 2048, 64), QUERY, QUERY),
+    ((1, 3, 2048, 64), WAVE, WAVE),
 ])
 def test_capi_planned_launches(gpu_sa, shape, plain, planned):
     q, kv, sink, idx, sc = case(*shape, seed=sum(shape))
@@ -192,7 +195,10 @@ def test_placed_tiles_match_ordered(gpu_sa, name):
     expect_plan(q, kv, idx, tiles=True)
     ntiles = q.shape[0] * -(-q.shape[1] // 8)
     assert 2 * ntiles >= cus and ntiles <= cus, "the shape must be in the placed regime"
-    assert k1 == INDEX | QUERY | TILE and k2 == QUERY | TILE
+    # topk <= 640: the per-query tiles run one wave per query, and a placed
+    # call has no order to make, so there is no QUERY launch
+    pq = WAVE if idx.shape[2] <= 640 else QUERY
+    assert k1 == INDEX | pq | TILE and k2 == pq | TILE
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     assert e1 == e2 == (1 if name == "mixed, bad index" else 0)
     if name == "high locality":  # and the values themselves, on a sample

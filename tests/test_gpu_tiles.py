@@ -92,8 +92,9 @@ def test_tile_duplicates_multiplicity(gpu_sa):
 
 def test_tile_reference_jump_falls_back(gpu_sa):
     """A column whose scores jump far above its first step's max makes the tile
-    hand itself to the per-query kernel (the tile kernel never rescales O):
-    that tile's queries then match the per-query path bit for bit."""
+    hand itself to the per-query code (the tile kernel never rescales O): that
+    tile's queries then match the plain per-query plan (one wave per query:
+    same math, other summation order) and the oracle."""
     # 256 queries: the plan must not split them, so the tile path runs
     q, kv, sink, idx, sc = rand_case(1, 256, 200, 128, seed=28)
     expect_plan(q, kv, idx, FORCE_TILES, tiles=True, nsplit=1)
@@ -102,7 +103,8 @@ def test_tile_reference_jump_falls_back(gpu_sa):
     idx[0, 2, 64] = 150                                     # later: a huge score
     o_t = run(q, kv, sink, idx, sc, flags=FORCE_TILES).cpu()
     o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY).cpu()
-    assert torch.equal(o_t[0, :8], o_p[0, :8])             # tile 0 ran per query
+    a8, p8 = o_t[0, :8].double(), o_p[0, :8].double()     # tile 0 ran per query
+    assert ((a8 - p8).pow(2).mean() / p8.pow(2).mean()).sqrt().item() <= 5e-3
     exp = sparse_attn_fp64(q, kv, sink, idx, sc)
     err = o_t.double().numpy() - exp
     rel = float(np.sqrt((err ** 2).mean() / (exp ** 2).mean()))
@@ -244,10 +246,15 @@ def test_per_query_tiles_mixed_with_aborted_tile(gpu_sa):
     o = run(q, kv, sink, idx, sc).cpu()
     o_p = run(q, kv, sink, idx, sc, flags=PER_QUERY).cpu()
     d = (o.float() - o_p.float()).abs()
+    d[0, 8:16] = 0  # |o| up to ~20 there: compared by relative RMS below
     say(f"  mixed list: max {d.max().item():.3e}")
     assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
-    assert torch.equal(o[0, 8:16], o_p[0, 8:16])   # the aborted tile ran per query
-    assert torch.equal(o[0, 32:], o_p[0, 32:])     # per-query tiles
+    # the aborted tile ran per query in the tile kernel (the 4-wave per-query
+    # code); the plain plan runs its queries one wave each: same math, other
+    # summation order
+    a8, p8 = o[0, 8:16].double(), o_p[0, 8:16].double()
+    assert ((a8 - p8).pow(2).mean() / p8.pow(2).mean()).sqrt().item() <= 5e-3
+    assert torch.equal(o[0, 32:], o_p[0, 32:])     # per-query tiles (wave kernel in both)
     sampled_check(o, q, kv, sink, idx, sc, [(0, t) for t in (0, 7, 16, 31, 40, 255)], "mixed")
     # row 2000 dominates queries 8..15 (|o| up to ~20, bf16 ulp 0.125 there):
     # relative RMS against float64 instead of the absolute bound

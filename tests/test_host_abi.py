@@ -129,9 +129,9 @@ def test_ctypes_binding_matches_header_layout():
         assert len(theirs._fields_) == len(mine._fields_)
         for (n1, _), (n2, _) in zip(theirs._fields_, mine._fields_):
             assert n1 == n2 and getattr(theirs, n1).offset == getattr(mine, n2).offset
-    assert sa_capi.KERNELS == ("index", "order", "tile", "query", "combine")
+    assert sa_capi.KERNELS == ("index", "order", "tile", "query", "combine", "wave")
     text = open(HEADER).read()
-    assert "SA_KERNEL_COUNT = 5" in text
+    assert "SA_KERNEL_COUNT = 6" in text
 
 
 def test_forward_events_rejects_bad_args_without_device_work(libs):
@@ -155,7 +155,7 @@ def test_library_exports_every_declared_symbol(libs):
     hip, _ = libs
     for name in declared_functions():
         assert hasattr(hip, name), f"{name} not exported"
-    assert hip.sa_abi_version() == 5
+    assert hip.sa_abi_version() == 6
 
 
 def test_strerror_covers_codes(libs):
