@@ -205,7 +205,7 @@ int sa_forward_noalloc(const sa_args* a, void* hip_stream);
  * the index kernel made per query, and makes the longest-first tile order
  * in its first work-group. (Version 5: the order no longer has a launch of
  * its own, so bit SA_KERNEL_ORDER is never set.) Version 6: unsplit plans
- * with topk <= 640 run their per-query
+ * with topk <= 384 run their per-query
  * queries as WAVE instead, one wave per query; in a tile plan that makes
  * the tile order needs, QUERY is then a one-work-group launch that only
  * makes it.

@@ -261,13 +261,22 @@ __device__ __forceinline__ void mfma_agpr(f32x16& c, bf16x8 a, bf16x8 b) {
       : "v"(a), "v"(b));
 }
 
-// v_mfma_f32_16x16x16_bf16 accumulating in AGPRs (the same hazards).
-__device__ __forceinline__ void mfma16_agpr(f32x4& c, bf16x4 a, bf16x4 b) {
+// v_mfma_f32_16x16x32_bf16 accumulating in VGPRs with its B operand in
+// AGPRs (an operand that lives in AGPRs for good, such as a resident Q^T,
+// then takes no VGPRs). The same hazards; the VALU reads of the result wait
+// for mfma_agpr_drain().
+__device__ __forceinline__ void mfma32_bagpr(f32x4& c, bf16x8 a, const bf16x8& b) {
   asm volatile(
       "s_nop 1\n\t"
-      "v_mfma_f32_16x16x16_bf16 %0, %1, %2, %0"
-      : "+a"(c)
-      : "v"(a), "v"(b));
+      "v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0"
+      : "+v"(c)
+      : "v"(a), "a"(b));
+}
+
+__device__ __forceinline__ f32x4 mfma_16x16x16(bf16x4 a, bf16x4 b, f32x4 c) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                  __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
 }
 
 __device__ __forceinline__ void mfma_agpr_drain() {
@@ -1382,7 +1391,11 @@ __global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
 constexpr int kWRows = 16;               // rows per step
 constexpr int kWPitch = kRowBytes + 48;  // LDS row pitch (bytes)
 constexpr int kWQueries = 2;             // queries per work-group
-constexpr int kWaveMaxTopk = 640;        // slots per query the list holds
+// Slots per query the list holds. Against the 4-wave per-query kernel: topk
+// 128 1365 -> 1102 us/call at 64 x 1024 queries, topk 640 1232 -> 1260 at
+// 1 x 16384 (a longer list amortises that kernel's start), so the cap sits
+// between them.
+constexpr int kWaveMaxTopk = 384;
 constexpr int kWSlots = kWaveMaxTopk / 64;
 static_assert(kTQ % kWQueries == 0, "a tile's queries split evenly");
 static_assert(kWQueries == 2, "the cursor state is two queries' scalars");
@@ -1604,9 +1617,9 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
           if (k + 3 < kDim / 32)
             kf[(k + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (k + 3));
           if (k & 1)
-            sb = mfma_16x16x32(kf[k & 3], qf[k], sb);
+            mfma32_bagpr(sb, kf[k & 3], qf[k]);
           else
-            sa = mfma_16x16x32(kf[k & 3], qf[k], sa);
+            mfma32_bagpr(sa, kf[k & 3], qf[k]);
           if constexpr (decltype(with_dma)::value) {
             const uint32_t off = uint32_t(__builtin_amdgcn_readlane(rv, k));
             lds_dma_row(kvs + off, 16 * lane, lnext + uint32_t(k * kWPitch));
@@ -1618,6 +1631,7 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
         s_chain(std::true_type{});
       else
         s_chain(std::false_type{});
+      mfma_agpr_drain();  // S^T is read by VALU below
       if (s == ns - 1 && jn < nq) load_q(jn);  // Q^T is no longer read
 
       // online softmax: lane (n, g) holds S[head n][row 4g + j]
@@ -1653,8 +1667,8 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
           for (int k = 0; k < 4; ++k) oacc[blk][k] *= ak[k];
       }
 
-      // O += P . V: lane (n, g) reads V[rows 4g .. 4g + 3][16 blk + n]; O in
-      // AGPRs, the V fragments of 16 column blocks read ahead of their MFMAs
+      // O += P . V: lane (n, g) reads V[rows 4g .. 4g + 3][16 blk + n]; the V
+      // fragments of 16 column blocks read ahead of their MFMAs
       const uint8_t* vb = tb + (4 * g + (n >> 2)) * kWPitch + 8 * (n & 3);
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -1662,11 +1676,10 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) vf[i] = lds_read_tr16(vb + 32 * (16 * h + i));
 #pragma unroll
-        for (int i = 0; i < 16; ++i) mfma16_agpr(oacc[16 * h + i], pb, vf[i]);
+        for (int i = 0; i < 16; ++i) oacc[16 * h + i] = mfma_16x16x16(pb, vf[i], oacc[16 * h + i]);
       }
     }
     if (ns > 0 && jn < nq) qloaded = jn;
-    mfma_agpr_drain();
     wave_epilogue(p, qb_of(j), qm_of(j), m_run, l_run, oacc);
     m_run = -INFINITY;
     l_run = 0.f;

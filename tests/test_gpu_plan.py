@@ -195,9 +195,9 @@ def test_placed_tiles_match_ordered(gpu_sa, name):
     expect_plan(q, kv, idx, tiles=True)
     ntiles = q.shape[0] * -(-q.shape[1] // 8)
     assert 2 * ntiles >= cus and ntiles <= cus, "the shape must be in the placed regime"
-    # topk <= 640: the per-query tiles run one wave per query, and a placed
+    # topk <= 384: the per-query tiles run one wave per query, and a placed
     # call has no order to make, so there is no QUERY launch
-    pq = WAVE if idx.shape[2] <= 640 else QUERY
+    pq = WAVE if idx.shape[2] <= 384 else QUERY
     assert k1 == INDEX | pq | TILE and k2 == pq | TILE
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     assert e1 == e2 == (1 if name == "mixed, bad index" else 0)

@@ -254,7 +254,7 @@ def test_per_query_tiles_mixed_with_aborted_tile(gpu_sa):
     # summation order
     a8, p8 = o[0, 8:16].double(), o_p[0, 8:16].double()
     assert ((a8 - p8).pow(2).mean() / p8.pow(2).mean()).sqrt().item() <= 5e-3
-    assert torch.equal(o[0, 32:], o_p[0, 32:])     # per-query tiles (wave kernel in both)
+    assert torch.equal(o[0, 32:], o_p[0, 32:])     # per-query tiles
     sampled_check(o, q, kv, sink, idx, sc, [(0, t) for t in (0, 7, 16, 31, 40, 255)], "mixed")
     # row 2000 dominates queries 8..15 (|o| up to ~20, bf16 ulp 0.125 there):
     # relative RMS against float64 instead of the absolute bound

@@ -1,5 +1,5 @@
 """GPU parity of the one-wave-per-query kernel (sa_fwd_wave_kernel): short
-unsplit queries (topk <= 640) of per-query plans and of the per-query tiles
+unsplit queries (topk <= 384) of per-query plans and of the per-query tiles
 of shared-row plans, checked against the float64 oracle on every query, with
 the launched-kernel mask of sa_forward_events naming the kernel that ran.
 
@@ -68,7 +68,7 @@ def per_query_queries(ws, b, m):
 @pytest.mark.parametrize("b,m,kv_len,topk,minus1", [
     (2, 160, 1024, 128, 0.0),    # contest-like prefill: every tile per query
     (1, 261, 4096, 100, 0.2),    # ragged last tile (5 queries: a one-query work-group)
-    (3, 89, 2048, 640, 0.1),     # the largest list; tiles of 8 + 1
+    (3, 89, 2048, 384, 0.1),     # the largest list; tiles of 8 + 1
     (1, 24, 600, 17, 0.0),       # one 16-row and one 1-row step (tiles shared here)
 ])
 def test_wave_tiles_full(gpu_sa, b, m, kv_len, topk, minus1):
@@ -144,9 +144,9 @@ def test_wave_bad_index_reported(gpu_sa):
     check(o, sparse_attn_fp64(q, kv, sink, ok, sc), "wave bad index")
 
 def test_wave_topk_cap(gpu_sa):
-    """topk 640 (the list's capacity) runs one wave per query; topk 641 runs
+    """topk 384 (the list's capacity) runs one wave per query; topk 385 runs
     the 4-wave per-query kernel. Both match the oracle."""
-    for topk, want in ((640, WAVE), (641, QUERY)):
+    for topk, want in ((384, WAVE), (385, QUERY)):
         q, kv, sink, idx, sc = case(1, 260, 3000, topk, seed=topk, minus1=0.1)
         if expect_plan(q, kv, idx, PER_QUERY, tiles=False)["nsplit"] != 1:
             pytest.skip("260 queries split on this device")
