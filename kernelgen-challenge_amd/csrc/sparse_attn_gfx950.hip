@@ -41,6 +41,12 @@
 //   read from the same LDS rows by ds_read_b64_tr_b16 transposing reads.
 //   Writes bf16 o, or per-part (max, sum, unnormalised O) for
 //   sa_combine_kernel.
+// sa_fwd_wave_kernel  unsplit queries with topk <= 384 (per-query tiles of
+//   shared-row plans, or every query of a per-query plan): one wave64 work-
+//   group per two queries, a stream of 16-row steps through the wave's own
+//   2-deep LDS-DMA ring, no barrier. S^T = K . Q^T (16x16x32 MFMA, Q^T as
+//   an AGPR operand), the softmax inside the wave, O += P . V with
+//   v_mfma_f32_16x16x16_bf16 taking P from the S^T accumulators.
 // sa_combine_kernel  merges the topk parts of one (query, head), folds the
 //   sink and stores bf16.
 // sa_merge_kernel  merges caller-supplied (o, lse) partials (sa_merge).
