@@ -18,13 +18,25 @@ Three timed loops of K calls each, all bracketed by ``torch.cuda.synchronize()``
   1. whole calls through the drop-in (``submission.sparse_attn``), timed with
      HIP events on the stream the kernels run on -> ``value``, ``ms_per_step``;
   2. the same calls through the C-ABI's event hook (``sa_forward_events``),
-     which records HIP events on that stream around every kernel it launches
-     -> the average launch duration of each kernel; the longest is the
-     dominant kernel, whose algorithmic work per launch / duration is
+     which launches every kernel through ``hipExtLaunchKernel`` with a pair
+     of HIP events that take the dispatch's own start and end timestamps (the
+     ones rocprofv3's kernel trace reads) on the stream the kernels run on
+     -> the average duration of each kernel; the longest is the dominant
+     kernel, whose algorithmic work per launch / duration is
      ``roofline.achieved``;
-  3. the calls of loop 1 with each input set's index plan
-     (``sparse_attn_plan``) made before the loop -> ``planned``: the cost of
-     a call whose indices are reused (not the headline ``value``).
+  3. plain calls and calls with each input set's index plan
+     (``sparse_attn_plan``, made before the loop) in alternating blocks, so
+     that neither is timed later in a drifting run -> ``planned``: the cost
+     of a call whose indices are reused (not the headline ``value``).
+
+``roofline.profile`` reads the committed rocprofv3 kernel-trace summary of the
+workload (``profiles/kernel_trace.json``): its average duration of the
+dominant kernel, the fraction that duration gives, and whether the summary
+was made from the sources this run uses (a SHA-256 digest of ``include/``,
+``kernelgen-challenge_amd/csrc/`` and ``build.py``, which both the
+summaries and this file compute). ``roofline.traffic`` is taken from
+``profiles/traffic.json`` only when its digest matches too; otherwise it is
+null, with the reason in ``roofline.traffic_note``.
 
 Printed: ONE JSON line (stdout). ``--all`` also prints one line per other
 configuration on stderr, and the track-02 lines below.
@@ -69,9 +81,9 @@ METRIC = ("sparse_attn µs/call, TFLOP/s + gathered-KV GB/s (% roofline) "
 PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 H, D = wl.NUM_HEADS, wl.HEAD_DIM
-KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel",
-                "tile": "sa_fwd_tile_kernel", "query": "sa_fwd_query_kernel",
-                "combine": "sa_combine_kernel", "wave": "sa_fwd_wave_kernel"}
+KERNEL_NAMES = {"index": "sa_tile_index_kernel", "tile": "sa_fwd_tile_kernel",
+                "query": "sa_fwd_query_kernel", "combine": "sa_combine_kernel",
+                "wave": "sa_fwd_wave_kernel"}
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the same
@@ -79,15 +91,44 @@ KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_tile_order_kernel"
 # profiles/traffic.json holds the figure per workload, with the commit whose
 # kernels were profiled and the summary (command, raw figures) it came from.
 TRAFFIC_JSON = os.path.join(REPO, "profiles", "traffic.json")
+# Average duration of each workload's dominant kernel in the committed
+# rocprofv3 --kernel-trace --stats summary of `bench.py --config <workload>`.
+KERNEL_TRACE_JSON = os.path.join(REPO, "profiles", "kernel_trace.json")
+# What the kernels are built from: a profile made from other files does not
+# describe this build.
+SOURCE_DIRS = (("include", (".h",)), (os.path.join("kernelgen-challenge_amd", "csrc"),
+                                      (".hip", ".h", ".cpp")))
+SOURCE_FILES = (os.path.join("kernelgen-challenge_amd", "build.py"),)
+
+
+def source_digest() -> str:
+    """SHA-256 (first 16 hex digits) over the relative path and bytes of
+    every kernel source, header and the build script, in sorted order."""
+    import hashlib
+    files = list(SOURCE_FILES)
+    for d, exts in SOURCE_DIRS:
+        files += [os.path.join(d, f) for f in os.listdir(os.path.join(REPO, d))
+                  if f.endswith(exts)]
+    h = hashlib.sha256()
+    for rel in sorted(files):
+        h.update(rel.replace(os.sep, "/").encode() + b"\0")
+        with open(os.path.join(REPO, rel), "rb") as f:
+            h.update(f.read())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
+def _profile_rec(path, workload):
+    try:
+        return json.load(open(path))["workloads"][workload]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def traffic_of(workload):
-    """(bytes per launch, commit, profile) of a workload's dominant kernel, or None."""
-    try:
-        rec = json.load(open(TRAFFIC_JSON))["workloads"][workload]
-    except (OSError, KeyError, ValueError):
-        return None
-    return rec["bytes_per_launch"], rec.get("commit"), rec.get("profile")
+    """The traffic.json record of a workload's dominant kernel (bytes per
+    launch, commit, sources digest, profile), or None."""
+    return _profile_rec(TRAFFIC_JSON, workload)
 
 
 def algorithmic(idx_cpu: torch.Tensor, b, m):
@@ -151,6 +192,19 @@ def time_calls(fn, sets, scale, steps, warmup, plans=None):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps  # ms per call
+
+
+def time_alternating(fn, sets, scale, steps, warmup, plans, rounds=4):
+    """ms per call of plain calls and of calls with plans, timed in `rounds`
+    alternating blocks (plain first in even rounds, planned first in odd
+    ones), so that neither variant runs later in the run than the other."""
+    per = max(1, steps // rounds)
+    tot = {False: 0.0, True: 0.0}
+    for r in range(rounds):
+        for planned in ((False, True) if r % 2 == 0 else (True, False)):
+            tot[planned] += time_calls(fn, sets, scale, per, warmup if r == 0 else 1,
+                                       plans=plans if planned else None) * per
+    return tot[False] / (per * rounds), tot[True] / (per * rounds), rounds
 
 
 def kernel_times(sets, scale, steps, warmup):
@@ -241,29 +295,49 @@ def cpu_baseline(cpu_inputs, target_s=4.0, runs=3):
             "us_per_call_extrapolated": round(dt / nq * b * m * 1e6, 1)}
 
 
-def roofline(name, flops, compulsory, times, shares):
+def roofline(name, flops, compulsory, times, shares, us_per_call):
     """The dominant kernel's algorithmic rate: its share of the call's flops
-    (or compulsory bytes) over its launch duration."""
+    (or compulsory bytes) over its average launch duration, measured in this
+    run (dispatch timestamps, see kernel_times). Beside it, the same rate
+    from the committed rocprofv3 trace summary of this workload, and whether
+    that summary and the traffic figure were made from this build's
+    sources."""
     dom = max(times, key=times.get)
     t = times[dom] * 1e-3
     mfma_bound = flops / (PEAK_MFMA_TFLOPS * 1e12) >= compulsory / (PEAK_HBM_GBPS * 1e9)
     share = shares.get(dom, 0.0)
-    if mfma_bound:
-        ach = flops * share / t / 1e12
-        roof = {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_MFMA_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_TFLOPS, 4)}
-    else:
-        ach = compulsory * share / t / 1e9
-        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBPS,
-                "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4)}
+    work, peak = (flops * share / 1e12, PEAK_MFMA_TFLOPS) if mfma_bound else \
+        (compulsory * share / 1e9, PEAK_HBM_GBPS)
+    ach = work / t
+    roof = {"bound": "mfma" if mfma_bound else "hbm", "achieved": round(ach, 3), "peak": peak,
+            "unit": "TFLOP/s" if mfma_bound else "GB/s", "frac": round(ach / peak, 4)}
+    digest = source_digest()
     tr = traffic_of(name)
-    roof["traffic"] = tr[0] if tr else None
-    if tr:
-        roof["traffic_commit"], roof["traffic_profile"] = tr[1], tr[2]
+    if tr and tr.get("sources") == digest:
+        roof["traffic"] = tr["bytes_per_launch"]
+        roof["traffic_profile"] = tr.get("profile")
+    else:
+        roof["traffic"] = None
+        roof["traffic_note"] = ("no traffic profile for this workload" if not tr else
+                                f"profiles/traffic.json was measured on sources {tr.get('sources')}, "
+                                f"this build is {digest}")
     roof["kernel"] = KERNEL_NAMES[dom]
     roof["kernel_us"] = round(times[dom] * 1e3, 2)
+    roof["kernel_timing"] = "HIP events taking the dispatch timestamps (hipExtLaunchKernel)"
+    if times[dom] * 1e3 > us_per_call:
+        # a kernel cannot outlast the call that launched it: the measurement is wrong
+        roof["frac"] = None
+        roof["frac_note"] = f"kernel_us {roof['kernel_us']} exceeds us_per_call {us_per_call}"
     roof["work_share"] = round(share, 4)
     roof["kernel_us_all"] = {KERNEL_NAMES[k]: round(v * 1e3, 2) for k, v in times.items()}
+    roof["sources"] = digest
+    prof = _profile_rec(KERNEL_TRACE_JSON, name)
+    if prof and prof.get("kernel", "").split("<")[0] == KERNEL_NAMES[dom]:
+        roof["profile"] = {"trace": prof.get("profile"), "kernel": prof.get("kernel"),
+                           "kernel_us": prof["avg_us"], "dispatches": prof.get("calls"),
+                           "frac": round(work / (prof["avg_us"] * 1e-6) / peak, 4),
+                           "live_over_profile": round(times[dom] * 1e3 / prof["avg_us"], 4),
+                           "sources_match": prof.get("sources") == digest}
     return roof
 
 
@@ -280,10 +354,12 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     settle_calls = settle(submission.sparse_attn, sets, scale, settle_s)
     ms = time_calls(submission.sparse_attn, sets, scale, steps, warmup)
     times, shares = kernel_times(sets, scale, steps, warmup)
-    # the same calls with each input set's index plan made beforehand
-    # (sparse_attn_plan): what a call costs when its indices are reused
+    # plain calls and calls with each input set's index plan made beforehand
+    # (sparse_attn_plan), in alternating blocks: what a call costs when its
+    # indices are reused, against the plain call timed the same way
     plans = [submission.sparse_attn_plan(s[0], s[1], s[3]) for s in sets]
-    ms_planned = time_calls(submission.sparse_attn, sets, scale, steps, warmup, plans=plans)
+    ms_rr_plain, ms_planned, rounds = time_alternating(
+        submission.sparse_attn, sets, scale, steps, warmup, plans)
     del plans
     t = ms * 1e-3
     tflops = flops / t / 1e12
@@ -311,10 +387,13 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                    "n_valid": n_valid, "unique_rows": uniq,
                    "flops_alg": flops, "gathered_bytes": gathered,
                    "compulsory_bytes": compulsory, "input_sets_rotated": nsets},
-        "roofline": roofline(name, flops, compulsory, times, shares),
+        "roofline": roofline(name, flops, compulsory, times, shares, round(ms * 1e3, 2)),
         "planned": {"us_per_call": round(ms_planned * 1e3, 2),
+                    "plain_us_per_call": round(ms_rr_plain * 1e3, 2),
                     "value": round(flops / (ms_planned * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
-                    "note": "index plan made before the timed calls and reused"},
+                    "note": (f"index plan made before the timed calls and reused; timed in "
+                             f"{rounds} alternating blocks of plain and planned calls "
+                             f"(plain_us_per_call: the plain calls of those blocks)")},
     }
     rec["cpu_baseline"] = cpu_baseline(cpu_inputs) if with_cpu else None
     del sets
@@ -558,14 +637,18 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
                     "unit": "GB/s", "frac": round(ach / PEAK_HBM_GBPS, 4)}
         tr = traffic_of(f"moe{MOE_WORKLOADS.index((label, M, K, N, E, topk))}") \
             if dom == "gateup" else None
+        if tr and tr.get("sources") != source_digest():
+            roof["traffic_note"] = (f"profiles/traffic.json was measured on sources "
+                                    f"{tr.get('sources')}, this build is {source_digest()}")
+            tr = None
         if tr:
-            roof.update({"traffic_commit": tr[1], "traffic_profile": tr[2]})
+            roof["traffic_profile"] = tr.get("profile")
         names = dict(MOE_KERNEL_NAMES, gateup=moe_gemm_kernel(M, N, E, topk, True),
                      down=moe_gemm_kernel(M, N, E, topk, False))
         if M <= MOE_FUSED_ROUTE_TOKENS:  # routing and plan in one launch
             times.pop("route", None)
             names["plan"] = "fm_route_plan_kernel"
-        roof.update({"traffic": tr[0] if tr else None, "kernel": names[dom],
+        roof.update({"traffic": tr["bytes_per_launch"] if tr else None, "kernel": names[dom],
                      "kernel_us": round(times[dom] * 1e3, 2),
                      "kernel_us_all": {names[k]: round(v * 1e3, 2) for k, v in times.items()}})
         rec = {"metric": "fused_moe µs/call, TFLOP/s + HBM GB/s (% roofline)",

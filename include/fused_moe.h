@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FM_ABI_VERSION 3
+#define FM_ABI_VERSION 4
 
 enum {
   FM_OK = 0,
@@ -45,8 +45,14 @@ enum {
 enum {
   FM_FLAG_LARGE_TILES = 1u,  /* 128-pair tiles whatever the tokens per expert */
   FM_FLAG_SMALL_TILES = 2u,  /* 16-pair weight-streaming tiles */
-  FM_FLAG_BIG_TILES = 4u     /* (ABI version 2) 256-pair tiles, 8 waves per work-group;
+  FM_FLAG_BIG_TILES = 4u,    /* (ABI version 2) 256-pair tiles, 8 waves per work-group;
                                 by default once experts average 256 pairs */
+  FM_FLAG_ORDERED_SUM = 8u   /* (ABI version 4) the final sum over a token's experts
+                                always runs as its own launch (the ascending-expert
+                                running bf16 sum), never as the down GEMM's bf16
+                                atomic adds into the output (topk <= 2 with
+                                streamed tiles); the result is the same bits.
+                                Combines with one tile flag. */
 };
 
 typedef struct fm_args {
@@ -91,9 +97,12 @@ enum {
   FM_KERNEL_COUNT = 5
 };
 
-/* Measurement hook (no counterpart in the reference): fm_forward that also
-   records events[2k] / events[2k + 1] (hipEvent_t, nullable entries) on the
-   stream right before / after kernel k and sets bit k of *launched. */
+/* Measurement hook (no counterpart in the reference): fm_forward that
+   launches kernel k through hipExtLaunchKernel with events[2k] /
+   events[2k + 1] (created hipEvent_t with timing; a kernel whose two entries
+   are NULL launches without events) as its start and stop events, which take
+   the dispatch's own start and end timestamps (ABI version 4; before, events
+   recorded on the stream around the launch), and sets bit k of *launched. */
 int fm_forward_events(const fm_args* a, void* hip_stream, void* const* events,
                       uint32_t* launched);
 

@@ -37,7 +37,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 6
+#define SA_ABI_VERSION 7
 
 /* Return codes. */
 enum {
@@ -180,23 +180,10 @@ int sa_merge(const sa_merge_args* a, void* hip_stream);
 int sa_plan_indices(const sa_args* a, void* hip_stream);
 
 /*
- * Allocation-free forward (ABI version 4). No counterpart in the reference:
- * it is for callers that cannot allocate device memory (code under HIP graph
- * capture, tight serving loops, harnesses that forbid hipMalloc). Same
- * arguments, results and launches as sa_forward, but the workspace is the
- * library's own device array of SA_NOALLOC_SCRATCH_BYTES (one per GPU, held
- * until the process ends); a->workspace and a->workspace_bytes are ignored.
- * It calls no allocating routine. A call whose sa_workspace_bytes exceeds
- * SA_NOALLOC_SCRATCH_BYTES returns SA_ESCRATCH before any device work (the
- * five configurations of the contest's hot path need at most ~40 MiB);
- * SA_FLAG_PLANNED is refused (SA_EINVAL): an index plan lives in a caller's
- * workspace. Every call on one GPU shares that GPU's array, so calls that
- * overlap on one GPU (other streams, other threads) race: serialize them.
- * Nothing in the array has to start at zero, and each call overwrites what
- * it reads before reading it.
+ * The allocation-free forward sa_forward_noalloc (ABI version 4) is declared
+ * in sparse_attn_noalloc.h and exported by its own library since version 7
+ * (see there); SA_ESCRATCH is its return code.
  */
-#define SA_NOALLOC_SCRATCH_BYTES (48u << 20)
-int sa_forward_noalloc(const sa_args* a, void* hip_stream);
 
 /*
  * Kernels of one sa_forward call. Launch order: per-query plans QUERY, then
@@ -223,13 +210,16 @@ enum {
 
 /*
  * Measurement hook. No counterpart in the reference, which times whole calls
- * from Python (track-01/bench.py:20-47). Same as sa_forward, and also records
- * events[2k] on hip_stream immediately before kernel k is launched and
- * events[2k + 1] immediately after it, for every kernel the call launches.
- * `events` holds 2 * SA_KERNEL_COUNT of the caller's hipEvent_t handles
- * (created with timing enabled; NULL entries are skipped). Bit k of
- * *launched (if non-null) is set when kernel k was launched. Nothing
- * synchronizes: read the events once the stream has drained.
+ * from Python (track-01/bench.py:20-47). Same as sa_forward, but kernel k is
+ * launched through hipExtLaunchKernel with events[2k] and events[2k + 1] as
+ * its start and stop events, which take the dispatch's own start and end
+ * timestamps (version 7; before, events recorded on the stream around the
+ * launch, which also timed the gap before the dispatch). `events` holds
+ * 2 * SA_KERNEL_COUNT of the caller's hipEvent_t handles (created, with
+ * timing enabled; a kernel whose two entries are NULL launches without
+ * events). Bit k of *launched (if non-null) is set when kernel k was
+ * launched. Nothing synchronizes: read the events once the stream has
+ * drained.
  */
 int sa_forward_events(const sa_args* a, void* hip_stream, void* const* events,
                       uint32_t* launched);

@@ -8,6 +8,10 @@ Outputs, all under ``kernelgen-challenge_amd/lib/``:
   C-ABI (``include/hc_sinkhorn.h``), built the same way.
 * ``libfused_moe_gfx950.so`` -- the track-03 ``fused_moe`` kernels + C-ABI
   (``include/fused_moe.h``), built the same way.
+* ``libsa_noalloc_gfx950.so`` -- the allocation-free entry point
+  ``sa_forward_noalloc`` (``include/sparse_attn_noalloc.h``) and its 48 MiB
+  device array, linked to ``libsparse_attn_gfx950.so``: only processes that
+  load it hold the array.
 * ``sa_torch_ext.so`` -- the PyTorch-ROCm operators ``torch.ops.sa_amd.*``
   (host C++ against torch's headers), linked to the two libraries above with
   an ``$ORIGIN`` rpath.
@@ -33,6 +37,7 @@ LIB_DIR = os.path.join(PKG_DIR, "lib")
 HIP_LIB = os.path.join(LIB_DIR, "libsparse_attn_gfx950.so")
 HC_LIB = os.path.join(LIB_DIR, "libhc_sinkhorn_gfx950.so")
 FM_LIB = os.path.join(LIB_DIR, "libfused_moe_gfx950.so")
+NOALLOC_LIB = os.path.join(LIB_DIR, "libsa_noalloc_gfx950.so")
 TORCH_EXT = os.path.join(LIB_DIR, "sa_torch_ext.so")
 HOST_TEST_LIB = os.path.join(LIB_DIR, "libsa_host_test.so")
 
@@ -82,6 +87,11 @@ def build_hip_lib(verbose=False):
         _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}",
               os.path.join(CSRC, src), "-o", tmp], verbose, strict=True)
         os.replace(tmp, out)
+    tmp = _atomic_target(NOALLOC_LIB)
+    _run([hipcc, *HIP_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}",
+          os.path.join(CSRC, "sa_noalloc_gfx950.hip"), f"-L{LIB_DIR}", "-lsparse_attn_gfx950",
+          "-Wl,-rpath,$ORIGIN", "-o", tmp], verbose, strict=True)
+    os.replace(tmp, NOALLOC_LIB)
 
 
 def build_torch_ext(verbose=False):
@@ -124,4 +134,5 @@ def build(verbose=False):
 
 if __name__ == "__main__":
     build(verbose="-q" not in sys.argv)
-    print(f"built {HIP_LIB}\n      {HC_LIB}\n      {FM_LIB}\n      {TORCH_EXT}\n      {HOST_TEST_LIB}")
+    print(f"built {HIP_LIB}\n      {HC_LIB}\n      {FM_LIB}\n      {NOALLOC_LIB}\n      {TORCH_EXT}\n"
+          f"      {HOST_TEST_LIB}")

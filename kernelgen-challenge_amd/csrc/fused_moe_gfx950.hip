@@ -35,9 +35,12 @@
 //   the tiles are streamed (decode): the routing launch clears out, and the
 //   down GEMM adds each weighted row into it with packed bf16 atomics (the
 //   two-term bf16 sum does not depend on the order).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+
+#include <type_traits>
 
 #include "fused_moe.h"
 
@@ -126,7 +129,8 @@ int validate(const fm_args* a) {
   if (a->K % kLargeCols != 0 || a->N % (kLargeCols / 2) != 0) return FM_EUNSUPPORTED;
   const uint32_t tile_flags = a->flags & (FM_FLAG_LARGE_TILES | FM_FLAG_SMALL_TILES |
                                           FM_FLAG_BIG_TILES);
-  if ((a->flags & ~tile_flags) != 0 || (tile_flags & (tile_flags - 1)) != 0)
+  if ((a->flags & ~(tile_flags | FM_FLAG_ORDERED_SUM)) != 0 ||
+      (tile_flags & (tile_flags - 1)) != 0)
     return FM_EINVAL;  // unknown bits, or more than one tile choice
   if (a->M == 0) return FM_OK;
   if (!a->hidden || !a->w1 || !a->w2 || !a->score || !a->out) return FM_EINVAL;
@@ -1250,13 +1254,24 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   if (a->M == 0) return FM_OK;
   const Plan pl = make_plan(a);
   if (a->workspace == nullptr || a->workspace_bytes < pl.bytes) return FM_EWORKSPACE;
-  auto mark = [&](int k, int after) -> bool {
-    if (after && launched != nullptr) *launched |= 1u << k;
-    if (events == nullptr) return true;
-    hipEvent_t ev = static_cast<hipEvent_t>(events[2 * k + after]);
-    return ev == nullptr || hipEventRecord(ev, stream) == hipSuccess;
+  // Launches kernel k (FM_KERNEL_*). With the caller's events, through
+  // hipExtLaunchKernel: events[2k] and events[2k+1] take the dispatch's own
+  // start and end timestamps.
+  auto run = [&](int k, const void* fn, dim3 grid, dim3 block, void** kargs) -> bool {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (events != nullptr) {
+      e0 = static_cast<hipEvent_t>(events[2 * k]);
+      e1 = static_cast<hipEvent_t>(events[2 * k + 1]);
+    }
+    const hipError_t err =
+        (e0 != nullptr || e1 != nullptr)
+            ? hipExtLaunchKernel(fn, grid, block, kargs, 0, stream, e0, e1, 0)
+            : hipLaunchKernel(fn, grid, block, kargs, 0, stream);
+    if (err != hipSuccess || hipGetLastError() != hipSuccess) return false;
+    if (launched != nullptr) *launched |= 1u << k;
+    return true;
   };
-  auto launched_ok = [&](int k) { return hipGetLastError() == hipSuccess && mark(k, 1); };
+  auto fn = [](auto kernel) { return reinterpret_cast<const void*>(kernel); };
   uint8_t* ws = static_cast<uint8_t*>(a->workspace);
   int32_t* ids = reinterpret_cast<int32_t*>(ws + pl.ids_off);
   float* wts = reinterpret_cast<float*>(ws + pl.wts_off);
@@ -1279,7 +1294,7 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   // into the output itself and the routing launch clears it: no final-sum
   // launch.
   const bool streamed = !pl.large && a->N % kStK == 0;  // (K % 256 == 0 always holds)
-  const bool fsum = streamed && a->topk <= 2;
+  const bool fsum = streamed && a->topk <= 2 && (a->flags & FM_FLAG_ORDERED_SUM) == 0;
   if (fsum) {
     rp.zero_out = static_cast<__bf16*>(a->out);
     rp.s_out = a->s_out;
@@ -1294,17 +1309,14 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   pp.E = int(a->E);
   pp.tile_rows = pl.tile_rows;
   if (a->M <= kFusedRouteTokens) {  // one launch, reported as the plan's
-    if (!mark(FM_KERNEL_PLAN, 0)) return FM_EHIP;
-    hipLaunchKernelGGL(fm_route_plan_kernel, dim3(1), dim3(1024), 0, stream, rp, pp);
-    if (!launched_ok(FM_KERNEL_PLAN)) return FM_EHIP;
+    void* ka[] = {&rp, &pp};
+    if (!run(FM_KERNEL_PLAN, fn(fm_route_plan_kernel), dim3(1), dim3(1024), ka)) return FM_EHIP;
   } else {
-    if (!mark(FM_KERNEL_ROUTE, 0)) return FM_EHIP;
-    hipLaunchKernelGGL(fm_route_kernel, dim3(unsigned((a->M + 3) / 4)), dim3(256), 0, stream,
-                       rp);
-    if (!launched_ok(FM_KERNEL_ROUTE)) return FM_EHIP;
-    if (!mark(FM_KERNEL_PLAN, 0)) return FM_EHIP;
-    hipLaunchKernelGGL(fm_plan_kernel, dim3(1), dim3(1024), 0, stream, pp);
-    if (!launched_ok(FM_KERNEL_PLAN)) return FM_EHIP;
+    void* kr[] = {&rp};
+    if (!run(FM_KERNEL_ROUTE, fn(fm_route_kernel), dim3(unsigned((a->M + 3) / 4)), dim3(256), kr))
+      return FM_EHIP;
+    void* kp[] = {&pp};
+    if (!run(FM_KERNEL_PLAN, fn(fm_plan_kernel), dim3(1), dim3(1024), kp)) return FM_EHIP;
   }
 
   GemmParams g1{};
@@ -1358,38 +1370,21 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   };
   const unsigned grid1 = grid_of(g1);
   const unsigned grid2 = grid_of(g2);
-  if (!mark(FM_KERNEL_GATEUP, 0)) return FM_EHIP;
-  if (pl.big)
-    hipLaunchKernelGGL(fm_gemm_big_kernel<true>, dim3(grid1), dim3(512), 0, stream, g1);
-  else if (pl.large)
-    hipLaunchKernelGGL(fm_gemm_kernel<true>, dim3(grid1), dim3(256), 0, stream, g1);
-  else if (streamed && pl.pb == 1)
-    hipLaunchKernelGGL((fm_stream_kernel<true, 1>), dim3(grid1), dim3(256), 0, stream, g1);
-  else if (streamed && pl.pb == 2)
-    hipLaunchKernelGGL((fm_stream_kernel<true, 2>), dim3(grid1), dim3(256), 0, stream, g1);
-  else if (streamed)
-    hipLaunchKernelGGL((fm_stream_kernel<true, 4>), dim3(grid1), dim3(256), 0, stream, g1);
-  else if (pl.pb == 1)
-    hipLaunchKernelGGL((fm_skinny_kernel<true, 1>), dim3(grid1), dim3(256), 0, stream, g1);
-  else
-    hipLaunchKernelGGL((fm_skinny_kernel<true, 2>), dim3(grid1), dim3(256), 0, stream, g1);
-  if (!launched_ok(FM_KERNEL_GATEUP)) return FM_EHIP;
-  if (!mark(FM_KERNEL_DOWN, 0)) return FM_EHIP;
-  if (pl.big)
-    hipLaunchKernelGGL(fm_gemm_big_kernel<false>, dim3(grid2), dim3(512), 0, stream, g2);
-  else if (pl.large)
-    hipLaunchKernelGGL(fm_gemm_kernel<false>, dim3(grid2), dim3(256), 0, stream, g2);
-  else if (streamed && pl.pb == 1)
-    hipLaunchKernelGGL((fm_stream_kernel<false, 1>), dim3(grid2), dim3(256), 0, stream, g2);
-  else if (streamed && pl.pb == 2)
-    hipLaunchKernelGGL((fm_stream_kernel<false, 2>), dim3(grid2), dim3(256), 0, stream, g2);
-  else if (streamed)
-    hipLaunchKernelGGL((fm_stream_kernel<false, 4>), dim3(grid2), dim3(256), 0, stream, g2);
-  else if (pl.pb == 1)
-    hipLaunchKernelGGL((fm_skinny_kernel<false, 1>), dim3(grid2), dim3(256), 0, stream, g2);
-  else
-    hipLaunchKernelGGL((fm_skinny_kernel<false, 2>), dim3(grid2), dim3(256), 0, stream, g2);
-  if (!launched_ok(FM_KERNEL_DOWN)) return FM_EHIP;
+  // the GEMM kernel of this plan, gated (gate-up) or not (down)
+  auto gemm = [&](auto gated) -> const void* {
+    constexpr bool G = decltype(gated)::value;
+    if (pl.big) return fn(fm_gemm_big_kernel<G>);
+    if (pl.large) return fn(fm_gemm_kernel<G>);
+    if (streamed)
+      return pl.pb == 1 ? fn(fm_stream_kernel<G, 1>)
+                        : pl.pb == 2 ? fn(fm_stream_kernel<G, 2>) : fn(fm_stream_kernel<G, 4>);
+    return pl.pb == 1 ? fn(fm_skinny_kernel<G, 1>) : fn(fm_skinny_kernel<G, 2>);
+  };
+  const dim3 gemm_block(pl.big ? 512 : 256);
+  void* k1[] = {&g1};
+  if (!run(FM_KERNEL_GATEUP, gemm(std::true_type{}), dim3(grid1), gemm_block, k1)) return FM_EHIP;
+  void* k2[] = {&g2};
+  if (!run(FM_KERNEL_DOWN, gemm(std::false_type{}), dim3(grid2), gemm_block, k2)) return FM_EHIP;
 
   if (fsum) return FM_OK;
   ReduceParams rd{};
@@ -1400,11 +1395,9 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
   rd.K = int(a->K);
   rd.topk = int(a->topk);
   const int64_t threads = a->M * (a->K / 8);
-  if (!mark(FM_KERNEL_REDUCE, 0)) return FM_EHIP;
-  hipLaunchKernelGGL(fm_reduce_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0,
-                     stream, rd);
-  if (!launched_ok(FM_KERNEL_REDUCE)) return FM_EHIP;
-  return FM_OK;
+  void* kd[] = {&rd};
+  return run(FM_KERNEL_REDUCE, fn(fm_reduce_kernel), dim3(unsigned((threads + 255) / 256)),
+             dim3(256), kd) ? FM_OK : FM_EHIP;
 }
 
 }  // namespace

@@ -50,6 +50,7 @@
 // sa_combine_kernel  merges the topk parts of one (query, head), folds the
 //   sink and stores bf16.
 // sa_merge_kernel  merges caller-supplied (o, lse) partials (sa_merge).
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -2260,31 +2261,6 @@ int current_cus(int* cus) {
   return SA_OK;
 }
 
-// Workspace of the allocation-free entry point (sa_forward_noalloc): one
-// array per GPU, created with the code object and held until the process
-// ends. Host code never passes `scratch` itself to a kernel (on the host the
-// name is only a stand-in for the symbol): it uses the device address that
-// hipGetSymbolAddress returns for the current device, looked up once per
-// device on that device's first sa_forward_noalloc call.
-constexpr size_t kScratchBytes = SA_NOALLOC_SCRATCH_BYTES;
-static __device__ __align__(256) uint8_t scratch[kScratchBytes];
-uint8_t* g_scratch[kMaxDevices];  // device address of `scratch`, per device ordinal
-
-int current_scratch(uint8_t** out) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return SA_EHIP;
-  uint8_t* p = __atomic_load_n(&g_scratch[dev], __ATOMIC_ACQUIRE);
-  if (p == nullptr) {
-    void* addr = nullptr;
-    if (hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)) != hipSuccess || addr == nullptr)
-      return SA_EHIP;
-    p = static_cast<uint8_t*>(addr);
-    __atomic_store_n(&g_scratch[dev], p, __ATOMIC_RELEASE);  // a racing thread stores the same
-  }
-  *out = p;
-  return SA_OK;
-}
-
 // What forward() launches: every kernel of a call, or only the index plan.
 enum class Launch { kCall, kPlanOnly };
 int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
@@ -2331,24 +2307,6 @@ int sa_forward_events(const sa_args* a, void* hip_stream, void* const* events,
                       uint32_t* launched) {
   if (launched != nullptr) *launched = 0u;
   return forward(a, static_cast<hipStream_t>(hip_stream), events, launched);
-}
-
-int sa_forward_noalloc(const sa_args* a, void* hip_stream) {
-  const int rc = sa::validate(a);
-  if (rc != SA_OK) return rc;
-  if ((a->flags & SA_FLAG_PLANNED) != 0) return SA_EINVAL;  // a plan lives in a caller's workspace
-  if (a->b == 0 || a->m == 0) return SA_OK;
-  int cus = 0;
-  const int qrc = current_cus(&cus);
-  if (qrc != SA_OK) return qrc;
-  if (sa::make_plan(a, cus).ws_bytes > kScratchBytes) return SA_ESCRATCH;
-  uint8_t* ws = nullptr;
-  const int src = current_scratch(&ws);
-  if (src != SA_OK) return src;
-  sa_args b = *a;
-  b.workspace = ws;
-  b.workspace_bytes = kScratchBytes;
-  return forward(&b, static_cast<hipStream_t>(hip_stream), nullptr, nullptr);
 }
 
 int sa_plan_indices(const sa_args* a, void* hip_stream) {
@@ -2409,12 +2367,27 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
   const sa::Plan plan = sa::make_plan(a, cus);
   if (plan.ws_bytes > 0 && (a->workspace == nullptr || a->workspace_bytes < plan.ws_bytes))
     return SA_EWORKSPACE;
-  auto mark = [&](int k, int after) -> bool {
-    if (after && launched != nullptr) *launched |= 1u << k;
-    if (events == nullptr) return true;
-    hipEvent_t ev = static_cast<hipEvent_t>(events[2 * k + after]);
-    return ev == nullptr || hipEventRecord(ev, stream) == hipSuccess;
+  // Launches kernel k (SA_KERNEL_*) with its one parameter block. With the
+  // caller's events, through hipExtLaunchKernel: events[2k] and events[2k+1]
+  // then take the dispatch's own start and end timestamps (the ones a
+  // kernel-trace profiler reads), not the stream position before and after
+  // it, which would add the gap before the dispatch.
+  auto run = [&](int k, const void* fn, dim3 grid, dim3 block, uint32_t lds, void* prm) -> int {
+    void* kargs[] = {prm};
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (events != nullptr) {
+      e0 = static_cast<hipEvent_t>(events[2 * k]);
+      e1 = static_cast<hipEvent_t>(events[2 * k + 1]);
+    }
+    const hipError_t err =
+        (e0 != nullptr || e1 != nullptr)
+            ? hipExtLaunchKernel(fn, grid, block, kargs, lds, stream, e0, e1, 0)
+            : hipLaunchKernel(fn, grid, block, kargs, lds, stream);
+    if (err != hipSuccess || hipGetLastError() != hipSuccess) return SA_EHIP;
+    if (launched != nullptr) *launched |= 1u << k;
+    return SA_OK;
   };
+  auto fn = [](auto kernel) { return reinterpret_cast<const void*>(kernel); };
   uint8_t* ws = static_cast<uint8_t*>(a->workspace);
   const float scale_log2 = a->scale * kLog2e;
 
@@ -2458,29 +2431,15 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
   // The per-query kernel; two work-groups per CU once there are at least two
   // per CU to run.
   auto launch_query = [&]() -> int {
-    if (p.meta == nullptr && wave_ok) {
-      if (!mark(SA_KERNEL_WAVE, 0)) return SA_EHIP;
-      hipLaunchKernelGGL(sa_fwd_wave_kernel, dim3(unsigned((p.nblocks + kWQueries - 1) / kWQueries)),
-                         dim3(64), 0, stream, p);
-      if (hipGetLastError() != hipSuccess) return SA_EHIP;
-      return mark(SA_KERNEL_WAVE, 1) ? SA_OK : SA_EHIP;
-    }
-    if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
+    if (p.meta == nullptr && wave_ok)
+      return run(SA_KERNEL_WAVE, fn(sa_fwd_wave_kernel),
+                 dim3(unsigned((p.nblocks + kWQueries - 1) / kWQueries)), dim3(64), 0, &p);
     const dim3 grid(unsigned(p.nblocks)), block(kThreads);
     const bool two = p.nblocks >= 2 * int64_t(cus);
-    if (p.meta != nullptr) {
-      if (two)
-        hipLaunchKernelGGL((sa_fwd_query_kernel<2, true>), grid, block, 0, stream, p);
-      else
-        hipLaunchKernelGGL((sa_fwd_query_kernel<4, true>), grid, block, 0, stream, p);
-    } else {
-      if (two)
-        hipLaunchKernelGGL((sa_fwd_query_kernel<2, false>), grid, block, 0, stream, p);
-      else
-        hipLaunchKernelGGL((sa_fwd_query_kernel<4, false>), grid, block, 0, stream, p);
-    }
-    if (hipGetLastError() != hipSuccess) return SA_EHIP;
-    return mark(SA_KERNEL_QUERY, 1) ? SA_OK : SA_EHIP;
+    const void* k = p.meta != nullptr
+                        ? (two ? fn(sa_fwd_query_kernel<2, true>) : fn(sa_fwd_query_kernel<4, true>))
+                        : (two ? fn(sa_fwd_query_kernel<2, false>) : fn(sa_fwd_query_kernel<4, false>));
+    return run(SA_KERNEL_QUERY, k, grid, block, 0, &p);
   };
 
   if (plan.tiles) {
@@ -2521,15 +2480,9 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
       if (lds > 65536 &&
           hipFuncSetAttribute(ik, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
         return SA_EHIP;
-      if (!mark(SA_KERNEL_INDEX, 0)) return SA_EHIP;
-      if (wide)
-        hipLaunchKernelGGL((sa_tile_index_kernel<1024, 2>), dim3(unsigned(plan.ntiles)), dim3(1024),
-                           lds, stream, ip);
-      else
-        hipLaunchKernelGGL((sa_tile_index_kernel<kIdxThreadsNarrow, kIdxVecNarrow>),
-                           dim3(unsigned(plan.ntiles)), dim3(kIdxThreadsNarrow), lds, stream, ip);
-      if (hipGetLastError() != hipSuccess) return SA_EHIP;
-      if (!mark(SA_KERNEL_INDEX, 1)) return SA_EHIP;
+      const int irc = run(SA_KERNEL_INDEX, ik, dim3(unsigned(plan.ntiles)),
+                          dim3(wide ? 1024 : kIdxThreadsNarrow), uint32_t(lds), &ip);
+      if (irc != SA_OK) return irc;
     }
     // The per-query launch: one work-group per tile runs the queries of a
     // per-query tile (the others return at once), and work-group 0 makes the
@@ -2551,17 +2504,14 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     if (wave_ok) {
       if (p.ord.order != nullptr) {
         p.nblocks = 1;
-        if (!mark(SA_KERNEL_QUERY, 0)) return SA_EHIP;
-        hipLaunchKernelGGL((sa_fwd_query_kernel<2, true>), dim3(1), dim3(kThreads), 0, stream, p);
-        if (hipGetLastError() != hipSuccess) return SA_EHIP;
-        if (!mark(SA_KERNEL_QUERY, 1)) return SA_EHIP;
+        const int orc = run(SA_KERNEL_QUERY, fn(sa_fwd_query_kernel<2, true>), dim3(1),
+                            dim3(kThreads), 0, &p);
+        if (orc != SA_OK) return orc;
         p.ord.order = nullptr;
       }
-      if (!mark(SA_KERNEL_WAVE, 0)) return SA_EHIP;
-      hipLaunchKernelGGL(sa_fwd_wave_kernel, dim3(unsigned(plan.ntiles * (kTQ / kWQueries))),
-                         dim3(64), 0, stream, p);
-      if (hipGetLastError() != hipSuccess) return SA_EHIP;
-      if (!mark(SA_KERNEL_WAVE, 1)) return SA_EHIP;
+      const int wrc = run(SA_KERNEL_WAVE, fn(sa_fwd_wave_kernel),
+                          dim3(unsigned(plan.ntiles * (kTQ / kWQueries))), dim3(64), 0, &p);
+      if (wrc != SA_OK) return wrc;
     } else {
       p.nblocks = what == Launch::kPlanOnly ? 1 : plan.ntiles + (p.ord.order != nullptr ? 1 : 0);
       const int lrc = launch_query();
@@ -2597,11 +2547,8 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.placed = placed ? 1 : 0;
     tp.meta = ip.meta;
     // One work-group per tile; those of per-query tiles return at once.
-    if (!mark(SA_KERNEL_TILE, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_fwd_tile_kernel, dim3(unsigned(plan.ntiles)), dim3(kThreads), 0,
-                       stream, tp);
-    if (hipGetLastError() != hipSuccess) return SA_EHIP;
-    return mark(SA_KERNEL_TILE, 1) ? SA_OK : SA_EHIP;
+    return run(SA_KERNEL_TILE, fn(sa_fwd_tile_kernel), dim3(unsigned(plan.ntiles)), dim3(kThreads),
+               0, &tp);
   }
   if (what == Launch::kPlanOnly) return SA_OK;  // per-query plans keep no index state
 
@@ -2621,11 +2568,9 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     c.sl_m = a->slse[1];
     c.sl_h = a->slse[2];
     c.nsplit = plan.nsplit;
-    if (!mark(SA_KERNEL_COMBINE, 0)) return SA_EHIP;
-    hipLaunchKernelGGL(sa_combine_kernel, dim3(unsigned(plan.units * kHeads)), dim3(64), 0,
-                       stream, c);
-    if (hipGetLastError() != hipSuccess) return SA_EHIP;
-    if (!mark(SA_KERNEL_COMBINE, 1)) return SA_EHIP;
+    const int crc = run(SA_KERNEL_COMBINE, fn(sa_combine_kernel),
+                        dim3(unsigned(plan.units * kHeads)), dim3(64), 0, &c);
+    if (crc != SA_OK) return crc;
   }
   return SA_OK;
 }

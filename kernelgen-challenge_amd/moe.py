@@ -18,13 +18,17 @@ from __future__ import annotations
 
 import torch
 
-__all__ = ["fused_moe", "FLAG_LARGE_TILES", "FLAG_SMALL_TILES", "FLAG_BIG_TILES"]
+__all__ = ["fused_moe", "FLAG_LARGE_TILES", "FLAG_SMALL_TILES", "FLAG_BIG_TILES",
+           "FLAG_ORDERED_SUM"]
 
 # Tile choice (fm_args.flags in include/fused_moe.h); 0 lets the library
 # choose from the tokens per expert.
 FLAG_LARGE_TILES = 1
 FLAG_SMALL_TILES = 2
 FLAG_BIG_TILES = 4
+# The final sum always as its own launch, never as atomic adds of the down
+# GEMM (same bits); combines with one tile flag.
+FLAG_ORDERED_SUM = 8
 
 _op = None  # the extension's fused_moe once it is loaded
 

@@ -15,6 +15,8 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "lib", "libsparse_attn_gfx950.so")
+# sa_forward_noalloc and its device array (include/sparse_attn_noalloc.h)
+NOALLOC_LIB_PATH = os.path.join(_HERE, "lib", "libsa_noalloc_gfx950.so")
 
 SA_OK, SA_EINVAL, SA_EUNSUPPORTED, SA_EWORKSPACE, SA_EHIP, SA_ESCRATCH = range(6)
 SA_NOALLOC_SCRATCH_BYTES = 48 << 20
@@ -60,7 +62,6 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sa_abi_version.argtypes = []
     lib.sa_workspace_bytes.argtypes = [args_p, ctypes.POINTER(ctypes.c_size_t)]
     lib.sa_forward.argtypes = [args_p, ctypes.c_void_p]
-    lib.sa_forward_noalloc.argtypes = [args_p, ctypes.c_void_p]
     lib.sa_forward_events.argtypes = [args_p, ctypes.c_void_p,
                                       ctypes.POINTER(ctypes.c_void_p),
                                       ctypes.POINTER(ctypes.c_uint32)]
@@ -68,6 +69,18 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.sa_plan_indices.argtypes = [args_p, ctypes.c_void_p]
     lib.sa_strerror.restype = ctypes.c_char_p
     lib.sa_strerror.argtypes = [ctypes.c_int]
+    return lib
+
+
+def noalloc_load(path: str = NOALLOC_LIB_PATH) -> ctypes.CDLL:
+    """Load the allocation-free entry point's library. Loading it reserves
+    SA_NOALLOC_SCRATCH_BYTES on each GPU the process uses it on."""
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(path)
+    lib.sa_forward_noalloc.argtypes = [ctypes.POINTER(SaArgs), ctypes.c_void_p]
+    lib.sa_noalloc_scratch_bytes.restype = ctypes.c_int
+    lib.sa_noalloc_scratch_bytes.argtypes = []
     return lib
 
 
@@ -167,7 +180,7 @@ def hc_make_args(mixes, scale, base, pre, post, comb, iters=20, eps=1e-6, flags=
 # ---------------------------------------------------------------------------
 FM_LIB_PATH = os.path.join(_HERE, "lib", "libfused_moe_gfx950.so")
 FM_OK, FM_EINVAL, FM_EUNSUPPORTED, FM_EWORKSPACE, FM_EHIP = range(5)
-FM_FLAG_LARGE_TILES, FM_FLAG_SMALL_TILES, FM_FLAG_BIG_TILES = 1, 2, 4
+FM_FLAG_LARGE_TILES, FM_FLAG_SMALL_TILES, FM_FLAG_BIG_TILES, FM_FLAG_ORDERED_SUM = 1, 2, 4, 8
 FM_KERNELS = ("route", "plan", "gateup", "down", "reduce")  # FM_KERNEL_* order
 FM_KERNEL_COUNT = len(FM_KERNELS)
 

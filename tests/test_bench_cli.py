@@ -57,12 +57,55 @@ def test_algorithmic_work():
 
 def test_tables():
     # traffic of every BASELINE config and every track-03 workload comes from
-    # a committed profile summary that names the commit it measured
+    # a committed profile summary that names the sources it measured
     for name in list(wl.CONFIGS) + [f"moe{i}" for i in range(len(bench.MOE_WORKLOADS))]:
         tr = bench.traffic_of(name)
-        assert tr is not None and tr[0] > 0, name
-        assert tr[1] and os.path.exists(os.path.join(bench.REPO, tr[2])), name
+        assert tr is not None and tr["bytes_per_launch"] > 0, name
+        assert os.path.exists(os.path.join(bench.REPO, tr["profile"])), name
     assert len(bench.MOE_WORKLOADS) == 8
     shapes = {(d, p) for _, d, _, p, _ in bench.HC_WORKLOADS}
     assert shapes == {((1, 1), (1, 16384)), ((16, 1), (16, 4096)), ((64, 1), (64, 1024))}
     assert [n for n, *_ in bench.HC_WORKLOADS] == ["16k-1k-1", "4k-1k-16", "1k-1k-64", "1k-1-64"]
+
+
+def test_source_digest_covers_kernel_sources(tmp_path, monkeypatch):
+    """The digest that stamps the profiles changes with any kernel source,
+    header or build flag, and with nothing else."""
+    import shutil
+    for rel in ("include", os.path.join("kernelgen-challenge_amd", "csrc")):
+        shutil.copytree(os.path.join(REPO, rel), tmp_path / rel)
+    shutil.copy(os.path.join(REPO, "kernelgen-challenge_amd", "build.py"),
+                tmp_path / "kernelgen-challenge_amd" / "build.py")
+    monkeypatch.setattr(bench, "REPO", str(tmp_path))
+    d0 = bench.source_digest()
+    assert d0 == bench.source_digest() and len(d0) == 16
+    (tmp_path / "README.md").write_text("not a source")
+    assert bench.source_digest() == d0
+    hip = tmp_path / "kernelgen-challenge_amd" / "csrc" / "sparse_attn_gfx950.hip"
+    hip.write_text(hip.read_text() + "\n")
+    d1 = bench.source_digest()
+    assert d1 != d0
+    hdr = tmp_path / "include" / "sparse_attn.h"
+    hdr.write_text(hdr.read_text() + " ")
+    assert bench.source_digest() not in (d0, d1)
+
+
+def test_roofline_record_checks_provenance(monkeypatch):
+    """frac comes from the live kernel time; the committed profile is quoted
+    beside it with its own frac; a traffic figure from other sources is
+    dropped with the reason; a kernel time above the call time voids frac."""
+    flops = 4.0 * 16 * 512 * 1000
+    monkeypatch.setattr(bench, "traffic_of", lambda name: {
+        "bytes_per_launch": 123, "sources": "0" * 16, "profile": "p.txt"})
+    monkeypatch.setattr(bench, "_profile_rec", lambda path, name: {
+        "kernel": "sa_fwd_tile_kernel", "avg_us": 100.0, "calls": 10, "profile": "t.txt",
+        "sources": bench.source_digest()})
+    r = bench.roofline("causal_prefill", flops, 1.0, {"tile": 0.1, "index": 0.02},
+                       {"tile": 1.0}, 130.0)
+    assert r["bound"] == "mfma" and r["kernel"] == "sa_fwd_tile_kernel"
+    assert abs(r["frac"] - flops / 100e-6 / 1e12 / 2500.0) < 1e-4
+    assert r["traffic"] is None and "traffic.json" in r["traffic_note"]
+    assert r["profile"]["sources_match"] and r["profile"]["kernel_us"] == 100.0
+    assert abs(r["profile"]["live_over_profile"] - 1.0) < 1e-9
+    r = bench.roofline("causal_prefill", flops, 1.0, {"tile": 0.2}, {"tile": 1.0}, 150.0)
+    assert r["frac"] is None and "exceeds" in r["frac_note"]

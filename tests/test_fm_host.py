@@ -45,7 +45,7 @@ def test_exports_every_declared_function(lib):
                           "fm_workspace_bytes"]
     for name in declared():
         assert hasattr(lib, name)
-    assert lib.fm_abi_version() == 3
+    assert lib.fm_abi_version() == 4
 
 
 def test_binding_matches_header_struct():
@@ -80,7 +80,7 @@ def args(M=4, K=256, N=128, E=8, topk=2):
     ("score", 0x40001, sa_capi.FM_EINVAL), ("s_hidden", 100, sa_capi.FM_EINVAL),
     ("s_score", 4, sa_capi.FM_EINVAL), ("flags", 3, sa_capi.FM_EINVAL),
     ("flags", 5, sa_capi.FM_EINVAL), ("flags", 6, sa_capi.FM_EINVAL),
-    ("flags", 8, sa_capi.FM_EINVAL),
+    ("flags", 16, sa_capi.FM_EINVAL), ("flags", 8 | 3, sa_capi.FM_EINVAL),
 ])
 def test_argument_errors_before_device_work(lib, field, value, code):
     a = args()

@@ -208,7 +208,7 @@ def test_capi_matches_operator_and_times_kernels(gpu_sa, shape, flags):
     hidden, w1, w2, score = make_inputs(M, K, N, E, seed=10)
     ref = op(hidden, w1, w2, score, topk, flags=flags)
     lib = sa_capi.fm_load()
-    assert lib.fm_abi_version() == 3
+    assert lib.fm_abi_version() == 4
     out = torch.full_like(hidden, float("nan"))
     a = sa_capi.fm_make_args(hidden, w1, w2, score, out, topk, flags=flags)
     n = sa_capi.fm_workspace_bytes(lib, a)
@@ -241,3 +241,52 @@ def test_capi_matches_operator_and_times_kernels(gpu_sa, shape, flags):
     rc = lib.fm_forward(ctypes.byref(a), ctypes.c_void_p(stream.cuda_stream))
     torch.cuda.synchronize()
     assert rc == sa_capi.FM_EWORKSPACE and torch.isnan(out).all()
+
+
+def _capi_run(hidden, w1, w2, score, topk, flags):
+    """fm_forward_events through the C-ABI: (output, launched-kernel mask)."""
+    lib = sa_capi.fm_load()
+    out = torch.full_like(hidden, float("nan"))
+    a = sa_capi.fm_make_args(hidden, w1, w2, score, out, topk, flags=flags)
+    n = sa_capi.fm_workspace_bytes(lib, a)
+    ws = torch.empty(n, dtype=torch.uint8, device=DEV)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), n
+    stream = torch.cuda.current_stream()
+    mask = sa_capi.fm_forward_events(lib, a, stream.cuda_stream,
+                                     [None] * (2 * sa_capi.FM_KERNEL_COUNT))
+    torch.cuda.synchronize()
+    return out, mask
+
+
+@pytest.mark.parametrize("shape", [(1, 2048, 1024, 8, 2), (64, 2048, 1024, 8, 2),
+                                   (64, 2048, 1024, 8, 1), (1, 2048, 1024, 8, 1),
+                                   (16, 512, 256, 8, 2)])
+@pytest.mark.parametrize("scale", ["normal", "subnormal"])
+def test_atomic_final_sum_equals_ordered_sum(shape, scale):
+    """With topk <= 2 and streamed tiles the down GEMM adds its bf16 products
+    into the output with packed bf16 atomics; FM_FLAG_ORDERED_SUM forces the
+    separate ascending-expert running sum instead. The two must agree bit for
+    bit: a two-term bf16 sum rounds the same exact value either way if the
+    atomic rounds to nearest even and keeps subnormals. Random bf16 addends
+    tie at the rounding point often (two values one binade apart leave one
+    extra bit, a tie half the time it is set), and the "subnormal" inputs put
+    the addends around the smallest normal bf16 (2^-126): hidden scaled by
+    2^-62 gives intermediate values near 2^-125 and outputs near 2^-127."""
+    M, K, N, E, topk = shape
+    hidden, w1, w2, score = make_inputs(M, K, N, E, seed=21)
+    if scale == "subnormal":
+        hidden = hidden * 2.0 ** -62
+    say(f"fused_moe atomic vs ordered sum M={M} K={K} N={N} E={E} topk={topk} {scale}")
+    out_a, mask_a = _capi_run(hidden, w1, w2, score, topk, 0)
+    out_o, mask_o = _capi_run(hidden, w1, w2, score, topk, sa_capi.FM_FLAG_ORDERED_SUM)
+    reduce = 1 << sa_capi.FM_KERNELS.index("reduce")
+    assert mask_a & reduce == 0, "the default path should add atomically here"
+    assert mask_o & reduce, "FM_FLAG_ORDERED_SUM must launch the final sum"
+    assert torch.equal(out_a.view(torch.int16), out_o.view(torch.int16))
+    if scale == "subnormal":
+        tiny = out_o.float().abs()
+        sub = ((tiny > 0) & (tiny < 2.0 ** -126)).sum().item()
+        assert sub > 0, "no subnormal outputs: the case does not test them"
+    # and both agree with the drop-in (operator path, default flags)
+    assert torch.equal(op(hidden, w1, w2, score, topk).view(torch.int16),
+                       out_a.view(torch.int16))

@@ -1,5 +1,6 @@
-"""GPU tests of the allocation-free entry point sa_forward_noalloc, through the
-C-ABI (ctypes): its output must equal sa_forward's (with a caller workspace)
+"""GPU tests of the allocation-free entry point sa_forward_noalloc
+(lib/libsa_noalloc_gfx950.so), through the C-ABI (ctypes): its output must
+equal sa_forward's (with a caller workspace)
 bit for bit, since both run the same kernels, on two calls in a row where the
 second input is smaller (the library's scratch array then holds the first
 call's contents). Each plan kind is covered: shared-row tiles, split-topk and
@@ -49,7 +50,7 @@ def noalloc(lib, q, kv, sink, idx, sc, flags=0):
     lse = torch.full(q.shape[:3], float("nan"), device=DEV)
     a = sa_capi.make_args(q, kv, sink, idx, o, sc, flags=flags, lse=lse)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    rc = lib.sa_forward_noalloc(ctypes.byref(a), stream)
+    rc = sa_capi.noalloc_load().sa_forward_noalloc(ctypes.byref(a), stream)
     torch.cuda.synchronize()
     return rc, o, lse
 
@@ -102,6 +103,7 @@ def test_noalloc_refuses_oversized_and_planned():
     assert sa_capi.workspace_bytes(lib, a) > sa_capi.SA_NOALLOC_SCRATCH_BYTES
     rc, o, _ = noalloc(lib, q, kv, sink, idx, sc)
     assert rc == sa_capi.SA_ESCRATCH
+    assert sa_capi.noalloc_load().sa_noalloc_scratch_bytes() == sa_capi.SA_NOALLOC_SCRATCH_BYTES
     assert "sa_forward_noalloc" in lib.sa_strerror(rc).decode()
     assert torch.isnan(o).all()  # nothing was launched
     q, kv, sink, idx, sc = case(1, 64, 700, 256, 9)
