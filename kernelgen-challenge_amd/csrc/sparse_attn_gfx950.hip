@@ -633,6 +633,68 @@ __device__ __forceinline__ void query_epilogue(const FwdParams& p, QuerySmemT<kR
   }
 }
 
+// Sorts the first kThreads * R entries of the LDS list `s` ascending, in
+// place: a bitonic network over kThreads * R keys, R consecutive keys per
+// thread. Entries at or past `n` count as +inf, so the n valid entries end up
+// in front, sorted; the caller reads no further. Steps whose partner key is
+// in the same thread compare registers, steps within a wave exchange them by
+// lane shuffles, and the steps across waves (partner distance >= 64 R) go
+// through the list itself between barriers. The result is the sorted
+// sequence, whatever order the entries came in. Not inlined: inside the
+// per-query unit, where Q^T and O are live, the unrolled network made the
+// compiler spill scalar registers and use scratch.
+template <int R>
+__device__ __attribute__((noinline)) void sort_list(int32_t* s, int n) {
+  constexpr int N = kThreads * R;
+  const int tid = threadIdx.x;
+  int v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = tid * R + r;
+    v[r] = i < n ? s[i] : INT32_MAX;
+  }
+  // the element of key position i keeps the smaller of the pair when the
+  // pair's run ascends and i is its lower position, or descends and i is not
+  auto keep = [](int mine, int other, int i, int k, int j) {
+    const bool up = (i & k) == 0, low = (i & j) == 0;
+    return up == low ? min(mine, other) : max(mine, other);
+  };
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if ((r & j) != 0) continue;
+          const int i = tid * R + r;
+          const int a = v[r], b = v[r | j];
+          const bool up = (i & k) == 0;
+          v[r] = up ? min(a, b) : max(a, b);
+          v[r | j] = up ? max(a, b) : min(a, b);
+        }
+      } else if (j < 64 * R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int o = __shfl_xor(v[r], j / R);
+          v[r] = keep(v[r], o, tid * R + r, k, j);
+        }
+      } else {
+        lds_barrier();  // every wave is past its last read of the list
+#pragma unroll
+        for (int r = 0; r < R; ++r) s[tid * R + r] = v[r];
+        lds_barrier();
+#pragma unroll
+        for (int r = 0; r < R; ++r) v[r] = keep(v[r], s[(tid * R + r) ^ j], tid * R + r, k, j);
+      }
+    }
+  }
+  lds_barrier();
+#pragma unroll
+  for (int r = 0; r < R; ++r) s[tid * R + r] = v[r];
+  lds_barrier();
+}
+
 // One (query, topk part) unit of the per-query kernel. Leaves every wave past
 // its last LDS access of `sm` only after the work-group's final barrier, so a
 // following unit may reuse `sm` after one more __syncthreads().
@@ -714,6 +776,23 @@ __device__ __forceinline__ void query_unit(const FwdParams& p, const int64_t uni
       if (vals[i] >= 0) s_list[pos++] = vals[i];
     __syncthreads();
     if (nvalid == 0) continue;
+    // An unsplit query walks its rows in ascending order. The queries of a
+    // launch that share a batch's kv then sweep it together, so a row that
+    // several of one XCD's queries name is fetched once into that XCD's L2
+    // and read there by the others, instead of each fetch landing at a
+    // random time. (A split query's parts run on many CUs at once, and a
+    // decode batch has one query: nothing to align.) Softmax and the sums
+    // do not depend on the slot order beyond the fp32 rounding of the sums.
+    if (p.nsplit == 1) {
+      if (nvalid <= kThreads)
+        sort_list<1>(s_list, nvalid);
+      else if (nvalid <= 2 * kThreads)
+        sort_list<2>(s_list, nvalid);
+      else if (nvalid <= 4 * kThreads)
+        sort_list<4>(s_list, nvalid);
+      else
+        sort_list<8>(s_list, nvalid);
+    }
     const int nsteps = (nvalid + kQRows - 1) / kQRows;
     // every load of this wave (Q) is complete before the gathers, whose
     // ring waits count only them
