@@ -59,7 +59,14 @@ enum {
   SA_FLAG_FORCE_TILES = 2u,
   /* (ABI version 3) the workspace holds the index plan of these arguments,
      made by sa_plan_indices: the index-dependent kernels are skipped */
-  SA_FLAG_PLANNED = 4u
+  SA_FLAG_PLANNED = 4u,
+  /* (ABI version 7) the form of the shared-row kernel's step. By default the
+     pair-skipping form runs when 8 * topk < kv_len (a row is then named by
+     fewer than one query of a tile on average, so query pairs often name no
+     row of a 32-row half-step and skip its P . V), the dense form otherwise.
+     These force one form; both give the same results. Not both at once. */
+  SA_FLAG_TILE_SKIP = 8u,
+  SA_FLAG_TILE_DENSE = 16u
 };
 
 /*

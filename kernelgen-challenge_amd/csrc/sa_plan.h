@@ -70,7 +70,10 @@ inline int validate(const sa_args* a) {
       a->topk < 0)
     return SA_EINVAL;
   if (a->h != kHeads || a->d != kDim) return SA_EUNSUPPORTED;
-  if ((a->flags & ~uint32_t(SA_FLAG_PER_QUERY | SA_FLAG_FORCE_TILES | SA_FLAG_PLANNED)) != 0)
+  if ((a->flags & ~uint32_t(SA_FLAG_PER_QUERY | SA_FLAG_FORCE_TILES | SA_FLAG_PLANNED |
+                            SA_FLAG_TILE_SKIP | SA_FLAG_TILE_DENSE)) != 0)
+    return SA_EINVAL;
+  if ((a->flags & SA_FLAG_TILE_SKIP) != 0 && (a->flags & SA_FLAG_TILE_DENSE) != 0)
     return SA_EINVAL;
   if (a->b == 0 || a->m == 0) return SA_OK;  // empty output, nothing to read
   if (a->q == nullptr || a->o == nullptr || a->sink == nullptr)

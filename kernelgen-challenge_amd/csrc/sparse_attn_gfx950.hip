@@ -1825,6 +1825,10 @@ union TileQuerySmem {
   QuerySmem q;
 };
 
+// kSkip: the pair-skipping form of the step (below, "Pair skipping"), for
+// tiles whose query pairs often name no row of a 32-row half-step; the dense
+// form otherwise. Their results are the same bits.
+template <bool kSkip>
 __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
   __shared__ __attribute__((aligned(16))) TileQuerySmem sm;
   auto& s_tile = sm.t.tile;
@@ -2029,6 +2033,25 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       lc0[a] = *reinterpret_cast<const f16x4*>(&lb[qw * kTileRows + 8 * a + 4 * hi]);
       lc1[a] = *reinterpret_cast<const f16x4*>(&lb[qw * kTileRows + 32 + 8 * a + 4 * hi]);
     }
+    // Pair skipping: the multiplicities of all 8 queries, 8 rows per lane
+    // (lane l: query l / 8, rows 8 (l % 8) ..), to tell which query pairs
+    // name a row of each half of the step.
+    uint4 lca;
+    if constexpr (kSkip)
+      lca = *reinterpret_cast<const uint4*>(&lb[(lane >> 3) * kTileRows + 8 * (lane & 7)]);
+    uint32_t act0 = 0xFu, act1 = 0xFu;  // bit j: queries 2j, 2j + 1 name a row of rows 0..31 / 32..63
+    // A named row's multiplicity is log2(count) >= 0 (sign bit clear), an
+    // unnamed one -inf (sign bit set).
+    auto pair_activity = [&]() {
+      const uint32_t all = lca.x & lca.y & lca.z & lca.w;
+      const uint64_t named = __ballot((all & 0x80008000u) != 0x80008000u);
+      act0 = act1 = 0u;
+#pragma unroll
+      for (int j = 0; j < kTQ / 2; ++j) {
+        act0 |= (named & (0x0F0Full << (16 * j))) != 0ull ? 1u << j : 0u;
+        act1 |= (named & (0xF0F0ull << (16 * j))) != 0ull ? 1u << j : 0u;
+      }
+    };
 
     // ---- S^T = K . Q^T, rows 0..31 then 32..63; the softmax of rows 0..31 runs
     // between the MFMAs of rows 32..63. All 16 rows of this wave's share of the
@@ -2062,6 +2085,7 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
           dma_row(rows_next, i / kDmaEvery, buf ^ 1);
         if (i == 1) dma_counts(nxt, buf ^ 1);
         if (i >= kDim / 16) sm_slot(i - kDim / 16, sacc0, lc0, 0, mx, mref, psum, pk);
+
         __builtin_amdgcn_sched_barrier(0);  // keep the interleave
       }
       l_run += psum;
@@ -2111,24 +2135,82 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       }
     };
 
-    // ---- O += P . V, rows 0..31, with the softmax of rows 32..63 -----------------
-    {
-      float mx = -INFINITY, mref = 0.f, psum = 0.f;
-      bf16x4 pk;
-      pv_half(0, [&]() { lds_barrier(); },  // P rows 0..31 of every column are in LDS
-              [&](int j) { sm_slot(j, sacc1, lc1, 1, mx, mref, psum, pk); });
-      l_run += psum;
-    }
-
-    // ---- O += P . V, rows 32..63 -------------------------------------------------
     int abort_seen = 0;
-    pv_half(2,
-            [&]() {
-              if (abort_any) s_abort = 1;
-              lds_barrier();  // P rows 32..63 are in LDS; every abort of this step is set
-              abort_seen = s_abort;
-            },
-            [](int) {});
+    if constexpr (!kSkip) {
+      // ---- O += P . V, rows 0..31, with the softmax of rows 32..63 ---------------
+      {
+        float mx = -INFINITY, mref = 0.f, psum = 0.f;
+        bf16x4 pk;
+        pv_half(0, [&]() { lds_barrier(); },  // P rows 0..31 of every column are in LDS
+                [&](int j) { sm_slot(j, sacc1, lc1, 1, mx, mref, psum, pk); });
+        l_run += psum;
+      }
+
+      // ---- O += P . V, rows 32..63 -----------------------------------------------
+      pv_half(2,
+              [&]() {
+                if (abort_any) s_abort = 1;
+                lds_barrier();  // P rows 32..63 are in LDS; every abort of this step is set
+                abort_seen = s_abort;
+              },
+              [](int) {});
+    } else {
+      // ---- Pair skipping: the softmax of rows 32..63 runs on its own (not
+      // interleaved with MFMAs), so that P of all 64 rows is in LDS after one
+      // barrier. Then O += P . V over the step's 64 rows, one 32-row half and
+      // one column block (query pair, 2 k-blocks x 4 d-blocks = 8 MFMAs) at a
+      // time: a block whose pair names no row of the half skips its MFMAs at
+      // the cost of one branch (its P is all zero there; with the dense form's
+      // interleaving such branches would sit around the softmax, and the
+      // compiler then spills its state). Per accumulator the MFMAs run in the
+      // dense form's order, so the sums are the same.
+      {
+        float mx = -INFINITY, mref = 0.f, psum = 0.f;
+        bf16x4 pk;
+#pragma unroll
+        for (int j = 0; j < kSmSlots; ++j) sm_slot(j, sacc1, lc1, 1, mx, mref, psum, pk);
+        l_run += psum;
+      }
+      pair_activity();
+      auto pread = [&](bf16x8 (&af)[2][4], int kb0) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int k = 0; k < 4; ++k)
+            af[kb][k] = *reinterpret_cast<const bf16x8*>(prd[k] + 32 * (kb0 + kb));
+      };
+      auto vread = [&](bf16x8 (&vf)[8], int kb0) {
+#pragma unroll
+        for (int n = 0; n < 8; ++n) {
+          const uint8_t* v0 = tb + voff + 16 * (kb0 + (n >> 2)) * kTilePitch + 64 * (n & 3);
+          const bf16x4 lo = lds_read_tr16(v0);
+          const bf16x4 up = lds_read_tr16(v0 + 4 * kTilePitch);
+          vf[n] = __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+      };
+      auto pv_blocks = [&](const bf16x8 (&af)[2][4], const bf16x8 (&vf)[8], uint32_t act) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (((act >> ((wave + k) & 3)) & 1u) != 0) {
+#pragma unroll
+            for (int n = 0; n < 8; ++n) {
+              mfma_agpr(oacc[4 * k + (n & 3)], af[n >> 2][k], vf[n]);
+              __builtin_amdgcn_sched_barrier(0);  // one MFMA per slot, in order
+            }
+          }
+        }
+      };
+      bf16x8 vf[8], af[2][4];
+      vread(vf, 0);  // V is in LDS since the gather barrier
+      if (abort_any) s_abort = 1;
+      lds_barrier();  // P rows 0..63 are in LDS; every abort of this step is set
+      abort_seen = s_abort;
+      pread(af, 0);
+      pv_blocks(af, vf, __builtin_amdgcn_readfirstlane(act0));
+      vread(vf, 2);
+      pread(af, 2);
+      pv_blocks(af, vf, __builtin_amdgcn_readfirstlane(act1));
+    }
 
     dma_barrier();  // every wave's prefetch has landed; P and this tile are free
     if (abort_seen != 0) {  // uniform: every wave read it after the same barrier
@@ -2626,8 +2708,13 @@ int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t*
     tp.placed = placed ? 1 : 0;
     tp.meta = ip.meta;
     // One work-group per tile; those of per-query tiles return at once.
-    return run(SA_KERNEL_TILE, fn(sa_fwd_tile_kernel), dim3(unsigned(plan.ntiles)), dim3(kThreads),
-               0, &tp);
+    // The pair-skipping form when a row is named by fewer than one query of a
+    // tile on average (high locality: 8 * 512 against 16 384 rows), unless a
+    // flag forces one form.
+    const bool skip = (a->flags & SA_FLAG_TILE_SKIP) != 0 ||
+                      ((a->flags & SA_FLAG_TILE_DENSE) == 0 && kTQ * a->topk < a->kv_len);
+    return run(SA_KERNEL_TILE, skip ? fn(sa_fwd_tile_kernel<true>) : fn(sa_fwd_tile_kernel<false>),
+               dim3(unsigned(plan.ntiles)), dim3(kThreads), 0, &tp);
   }
   if (what == Launch::kPlanOnly) return SA_OK;  // per-query plans keep no index state
 

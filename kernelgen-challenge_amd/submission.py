@@ -41,6 +41,7 @@ __all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "sparse_a
            "IndexPlan", "set_index_check", "index_check_enabled", "index_check_mode",
            "check_index_errors", "set_path_flags",
            "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES",
+           "FLAG_TILE_SKIP", "FLAG_TILE_DENSE",
            "hc_split_sinkhorn", "fused_moe"]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -68,6 +69,8 @@ _err_flags = {}  # device index -> ctypes int32 over the mapped host flag
 # Kernel-path selection bits, as sa_args.flags in include/sparse_attn.h.
 FLAG_PER_QUERY = 1     # every query gathers its own rows
 FLAG_FORCE_TILES = 2   # every eligible 8-query tile shares its row union
+FLAG_TILE_SKIP = 8     # shared tiles use the pair-skipping step (same results)
+FLAG_TILE_DENSE = 16   # shared tiles use the dense step (same results)
 
 
 def extension_path() -> str:

@@ -263,3 +263,76 @@ def test_per_query_tiles_mixed_with_aborted_tile(gpu_sa):
     rel = float(np.sqrt((err ** 2).mean() / (exp ** 2).mean()))
     say(f"  aborted tile: rel_rms={rel:.3e}")
     assert rel <= 5e-3
+
+
+TILE_SKIP, TILE_DENSE = 8, 16
+
+
+def run_lse(q, kv, sink, idx, scale, flags):
+    err = torch.zeros(1, dtype=torch.int32, device=DEV)
+    o, lse = torch.ops.sa_amd.sparse_attn_fwd_lse(q.to(DEV), kv.to(DEV), sink.to(DEV),
+                                                  idx.to(DEV), float(scale), err, flags)
+    assert int(err.item()) == 0
+    return o, lse
+
+
+def windows_case(b, m, kv_len, nwin, seed, keep=0.75):
+    """High-locality-style indices: each query takes nwin 64-row windows,
+    keeping the previous query's starts with probability `keep`."""
+    q, kv, sink, idx, sc = rand_case(b, m, kv_len, 64 * nwin, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    for bi in range(b):
+        starts = 64 * torch.randperm(kv_len // 64, generator=g)[:nwin]
+        for t in range(m):
+            if t and torch.rand(1, generator=g).item() >= keep:
+                starts = 64 * torch.randperm(kv_len // 64, generator=g)[:nwin]
+            s = torch.sort(starts).values
+            idx[bi, t] = (s[:, None] + torch.arange(64)[None]).reshape(-1).to(torch.int32)
+    return q, kv, sink, idx, sc
+
+
+def skip_cases():
+    cases = {"windows": windows_case(2, 64, 8192, 6, seed=41),
+             "dense random": rand_case(1, 64, 512, 256, seed=42, minus1=0.3),
+             "ragged m": rand_case(1, 13, 2048, 64, seed=43, minus1=0.1)}
+    # duplicates, -1 padding in the middle of rows, an all-masked tile and a
+    # tile whose union ends inside a 64-row step
+    q, kv, sink, idx, sc = windows_case(1, 40, 4096, 3, seed=44)
+    idx[0, 3, 5:20] = idx[0, 3, 0]        # one row named 16 times
+    idx[0, 9, ::3] = -1
+    idx[0, 16:24] = -1                    # tile 2: no valid slot
+    idx[0, 32:40, 100:] = -1              # tile 4: 100 slots per query
+    cases["edge"] = (q, kv, sink, idx, sc)
+    return cases
+
+
+@pytest.mark.parametrize("name", ["windows", "dense random", "ragged m", "edge"])
+def test_tile_forms_bit_identical(gpu_sa, name):
+    """The pair-skipping and the dense form of the shared-row step give the
+    same bits (o and lse): per accumulator they run the same MFMAs in the same
+    order, and a skipped block would only add zeros. Both are also held to
+    the float64 oracle on a sample."""
+    q, kv, sink, idx, sc = skip_cases()[name]
+    o_s, l_s = run_lse(q, kv, sink, idx, sc, FORCE_TILES | TILE_SKIP)
+    o_d, l_d = run_lse(q, kv, sink, idx, sc, FORCE_TILES | TILE_DENSE)
+    assert torch.equal(o_s, o_d) and torch.equal(l_s, l_d)
+    b, m = idx.shape[:2]
+    sel = sorted({(bi, t) for bi in range(b) for t in (0, 1, 7, 8, 17, m - 1) if t < m})
+    sampled_check(o_s, q, kv, sink, idx, sc, sel, f"tile skip form, {name}")
+
+
+def test_tile_forms_aborted_tile(gpu_sa):
+    """A tile whose scores jump above its reference aborts to the per-query
+    code in both forms; the outputs agree bit for bit."""
+    q, kv, sink, idx, sc = windows_case(1, 16, 4096, 4, seed=45)
+    idx[0, 8:16, -1] = 2000
+    kv[0, 2000] = (q[0, 8].float().mean(0) * 60).to(torch.bfloat16)
+    o_s = run(q, kv, sink, idx, sc, flags=FORCE_TILES | TILE_SKIP)
+    o_d = run(q, kv, sink, idx, sc, flags=FORCE_TILES | TILE_DENSE)
+    assert torch.equal(o_s, o_d)
+
+
+def test_tile_form_flags_refused_together(gpu_sa):
+    q, kv, sink, idx, sc = rand_case(1, 8, 256, 32, seed=46)
+    with pytest.raises((ValueError, RuntimeError)):
+        run(q, kv, sink, idx, sc, flags=TILE_SKIP | TILE_DENSE)

@@ -114,7 +114,9 @@ def test_plan_indices_rejects_bad_args_without_device_work(libs):
     a.d = 256
     assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EUNSUPPORTED
     a = good_args()
-    a.flags = 8
+    a.flags = 32
+    assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EINVAL
+    a.flags = 8 | 16                           # both tile forms at once
     assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EINVAL
     a = good_args(b=0)                         # empty: nothing to plan
     assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_OK
@@ -212,7 +214,8 @@ def test_forward_rejects_null_args(libs):
     ("q", 0, SA_EINVAL), ("o", 0, SA_EINVAL), ("sink", 0, SA_EINVAL),
     ("idx", 0, SA_EINVAL), ("kv", 0, SA_EINVAL),
     ("q", 0x10008, SA_EINVAL), ("o", 0x50002, SA_EINVAL), ("kv", 0x20004, SA_EINVAL),
-    ("scale", float("nan"), SA_EINVAL), ("flags", 8, SA_EINVAL), ("flags", 1 << 31, SA_EINVAL),
+    ("scale", float("nan"), SA_EINVAL), ("flags", 32, SA_EINVAL), ("flags", 8 | 16, SA_EINVAL),
+    ("flags", 1 << 31, SA_EINVAL),
 ])
 def test_forward_argument_errors(libs, field, value, code):
     hip, host = libs
