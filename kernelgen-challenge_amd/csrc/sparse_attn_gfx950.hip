@@ -1591,6 +1591,17 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
 #pragma unroll
     for (int s = 0; s < kDim / 32; ++s) qf[s] = *reinterpret_cast<const bf16x8*>(qrow + 32 * s);
   };
+  // Q^T as the B operand of S^T lives in AGPRs: qa is written from qf once
+  // per query (the tied asm operand makes the compiler copy qf into the
+  // AGPRs there), and the MFMAs read it with an "a" constraint. Read straight
+  // from qf, the MFMAs made the compiler copy Q^T into AGPRs at every step
+  // (64 v_accvgpr_write per step), since qf changes inside the step loop when
+  // the next query's Q^T is loaded.
+  bf16x8 qa[kDim / 32];
+  auto q_to_agpr = [&]() {
+#pragma unroll
+    for (int s = 0; s < kDim / 32; ++s) asm volatile("" : "=a"(qa[s]) : "0"(qf[s]));
+  };
   load_q(0);
 
   // ---- compaction: query j's valid slots at list[qsel(j) .. qsel(j + 1)) ----------
@@ -1683,6 +1694,7 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
       // and the reads of the buffer the next gathers fill are complete
       __builtin_amdgcn_s_waitcnt(0x0070);  // vmcnt(0) lgkmcnt(0)
       asm volatile("" ::: "memory");
+      if (s == 0) q_to_agpr();  // this query's Q^T, landed
       const bool dma = gstep + 1 < total;
       const int rv = dma ? cursor_rows() : 0;
       const uint8_t* kvs = kv_scalar();
@@ -1703,9 +1715,9 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
           if (k + 3 < kDim / 32)
             kf[(k + 3) & 3] = *reinterpret_cast<const bf16x8*>(krow + 64 * (k + 3));
           if (k & 1)
-            mfma32_bagpr(sb, kf[k & 3], qf[k]);
+            mfma32_bagpr(sb, kf[k & 3], qa[k]);
           else
-            mfma32_bagpr(sa, kf[k & 3], qf[k]);
+            mfma32_bagpr(sa, kf[k & 3], qa[k]);
           if constexpr (decltype(with_dma)::value) {
             const uint32_t off = uint32_t(__builtin_amdgcn_readlane(rv, k));
             lds_dma_row(kvs + off, 16 * lane, lnext + uint32_t(k * kWPitch));
