@@ -22,6 +22,12 @@
  *                      raises here (torch.gather at reference.py:28); the
  *                      Python layer turns the flag into RuntimeError.
  *
+ * Shapes (ABI version 7): d = 512; h = 1, 2, 4, 8 or a multiple of 16 (the
+ * reference's kernels take power-of-two h, track-01/submission.py:1004,
+ * :1233; the contest fixes h = 16). The kernels compute 16 heads at a time:
+ * 16 k heads run as k passes over 16-head slices, and fewer heads on a
+ * zero-padded 16-head copy in the workspace (sa_workspace_bytes counts it).
+ *
  * Threading and ownership: the caller owns every buffer. The library keeps no
  * mutable state apart from a per-device cache of the compute-unit count, and
  * every entry point is reentrant. sa_forward is asynchronous on the given
@@ -43,7 +49,8 @@ extern "C" {
 enum {
   SA_OK = 0,
   SA_EINVAL = 1,        /* null pointer, negative size, bad stride or alignment */
-  SA_EUNSUPPORTED = 2,  /* h != 16, d != 512, or a grid beyond the launch limit */
+  SA_EUNSUPPORTED = 2,  /* h not 1, 2, 4, 8 or a multiple of 16; d != 512; or a
+                           grid beyond the launch limit */
   SA_EWORKSPACE = 3,    /* workspace missing or smaller than sa_workspace_bytes */
   SA_EHIP = 4,          /* HIP runtime error (device query or launch) */
   SA_ESCRATCH = 5       /* (ABI version 4) sa_forward_noalloc: the call needs more

@@ -9,6 +9,16 @@ int sa_host_validate(const sa_args* a) { return sa::validate(a); }
 
 int sa_host_validate_merge(const sa_merge_args* a) { return sa::validate_merge(a); }
 
+// sa_workspace_bytes with a given CU count: the plan's bytes and, below 16
+// heads, the 16-head copy of q and o (sa::pad_layout).
+int sa_host_workspace_bytes(const sa_args* a, int num_cus, int64_t* out) {
+  const int rc = sa::validate(a);
+  if (rc != SA_OK) return rc;
+  const size_t plan = sa::make_plan(a, num_cus).ws_bytes;
+  *out = int64_t(plan + sa::pad_layout(a, plan).bytes);
+  return SA_OK;
+}
+
 int sa_host_plan(const sa_args* a, int num_cus, int64_t* nsplit, int64_t* split_len,
                  size_t* ws_bytes) {
   const int rc = sa::validate(a);

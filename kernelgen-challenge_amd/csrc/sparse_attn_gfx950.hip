@@ -2411,6 +2411,57 @@ __global__ void __launch_bounds__(256) sa_merge_kernel(const MergeParams p) {
   }
 }
 
+// ============================================================================
+// head padding (calls with 1, 2, 4 or 8 heads)
+// ============================================================================
+// The kernels compute 16 heads. A call with fewer runs on a 16-head copy in
+// its workspace: q padded with zero heads (and 16 sink entries), then the
+// first h heads of the 16-head o (and lse) copied out. One thread per 8
+// elements of a head's row; the padded heads' outputs are never read.
+struct PadParams {
+  const __bf16* q;     // [b, m, h, d], strides sq_*
+  const float* sink;   // [h]
+  __bf16* qp;          // [b * m, 16, d] contiguous
+  float* sinkp;        // [16]
+  const __bf16* op;    // [b * m, 16, d] contiguous
+  const float* lsep;   // [b * m, 16] or null
+  __bf16* o;           // [b, m, h, d], strides so_*
+  float* lse;          // [b, m, h], strides sl_*, or null
+  int64_t m, h, rows;  // rows = b * m * (16 for the pad, h for the unpad)
+  int64_t sq_b, sq_m, sq_h, so_b, so_m, so_h, sl_b, sl_m, sl_h;
+};
+
+__global__ void __launch_bounds__(256) sa_pad_heads_kernel(const PadParams p) {
+  const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (t < kHeads) p.sinkp[t] = t < p.h ? p.sink[t] : 0.f;
+  if (t >= p.rows * (kDim / 8)) return;
+  const int64_t r = t / (kDim / 8);  // (b * m) * 16 + head
+  const int c = int(t % (kDim / 8));
+  const int64_t bm = r / kHeads, hh = r % kHeads;
+  bf16x8 v;
+  if (hh < p.h) {
+    const int64_t bi = bm / p.m, mi = bm % p.m;
+    v = *reinterpret_cast<const bf16x8*>(p.q + bi * p.sq_b + mi * p.sq_m + hh * p.sq_h + 8 * c);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = static_cast<__bf16>(0.f);
+  }
+  *reinterpret_cast<bf16x8*>(p.qp + r * kDim + 8 * c) = v;
+}
+
+__global__ void __launch_bounds__(256) sa_unpad_heads_kernel(const PadParams p) {
+  const int64_t t = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= p.rows * (kDim / 8)) return;
+  const int64_t r = t / (kDim / 8);  // (b * m) * h + head
+  const int c = int(t % (kDim / 8));
+  const int64_t bm = r / p.h, hh = r % p.h;
+  const int64_t bi = bm / p.m, mi = bm % p.m;
+  const int64_t src = bm * kHeads + hh;
+  *reinterpret_cast<bf16x8*>(p.o + bi * p.so_b + mi * p.so_m + hh * p.so_h + 8 * c) =
+      *reinterpret_cast<const bf16x8*>(p.op + src * kDim + 8 * c);
+  if (c == 0 && p.lse != nullptr) p.lse[bi * p.sl_b + mi * p.sl_m + hh * p.sl_h] = p.lsep[src];
+}
+
 // Compute units of the current device, cached per device ordinal.
 constexpr int kMaxDevices = 64;
 int g_cus[kMaxDevices];  // 0 = not yet queried (benign race: same value)
@@ -2438,6 +2489,9 @@ int current_cus(int* cus) {
 enum class Launch { kCall, kPlanOnly };
 int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
             Launch what = Launch::kCall);
+// The same for 16 heads (forward() runs other head counts through it).
+int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
+              Launch what);
 
 }  // namespace
 
@@ -2449,7 +2503,8 @@ const char* sa_strerror(int code) {
   switch (code) {
     case SA_OK: return "ok";
     case SA_EINVAL: return "invalid argument (null pointer, size, stride, alignment or flags)";
-    case SA_EUNSUPPORTED: return "unsupported shape (needs h == 16, d == 512)";
+    case SA_EUNSUPPORTED:
+      return "unsupported shape (needs h = 1, 2, 4, 8 or a multiple of 16, and d = 512)";
     case SA_EWORKSPACE: return "workspace missing or too small";
     case SA_EHIP: return "HIP runtime error";
     case SA_ESCRATCH:
@@ -2468,7 +2523,8 @@ int sa_workspace_bytes(const sa_args* a, size_t* out_bytes) {
   int cus = 0;
   const int qrc = current_cus(&cus);
   if (qrc != SA_OK) return qrc;
-  *out_bytes = sa::make_plan(a, cus).ws_bytes;
+  const size_t plan_bytes = sa::make_plan(a, cus).ws_bytes;
+  *out_bytes = plan_bytes + sa::pad_layout(a, plan_bytes).bytes;
   return SA_OK;
 }
 
@@ -2529,8 +2585,87 @@ namespace {
 // on the stream around kernel k (SA_KERNEL_*) and sets bit k of *launched.
 // SA_FLAG_PLANNED skips the index kernels (their results are in the
 // workspace); Launch::kPlanOnly runs only them.
+// 16 heads: the kernels directly. 16 k heads: k calls on 16-head slices of
+// q, sink, o and lse (strided views; the plan is head-independent, so an
+// index plan serves every slice). 1, 2, 4 or 8 heads: a 16-head copy in the
+// workspace after the plan's bytes (sa::pad_layout), zero-padded q in, the
+// first h heads of o (and lse) out.
 int forward(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
             Launch what) {
+  const int rc = sa::validate(a);
+  if (rc != SA_OK) return rc;
+  if (a->h == kHeads || a->b == 0 || a->m == 0) return forward16(a, stream, events, launched, what);
+  if (a->h > kHeads) {
+    for (int64_t g = 0; g < a->h / kHeads; ++g) {
+      sa_args s = *a;
+      s.h = kHeads;
+      s.q = static_cast<const __bf16*>(a->q) + g * kHeads * a->sq[2];
+      s.o = static_cast<__bf16*>(a->o) + g * kHeads * a->so[2];
+      s.sink = a->sink + g * kHeads;
+      if (a->lse != nullptr) s.lse = a->lse + g * kHeads * a->slse[2];
+      const int grc = forward16(&s, stream, events, launched, what);
+      if (grc != SA_OK || what == Launch::kPlanOnly) return grc;
+    }
+    return SA_OK;
+  }
+  int cus = 0;
+  const int qrc = current_cus(&cus);
+  if (qrc != SA_OK) return qrc;
+  const size_t plan_bytes = sa::make_plan(a, cus).ws_bytes;
+  const sa::PadLayout pl = sa::pad_layout(a, plan_bytes);
+  if (a->workspace == nullptr || a->workspace_bytes < plan_bytes + pl.bytes) return SA_EWORKSPACE;
+  uint8_t* ws = static_cast<uint8_t*>(a->workspace);
+  sa_args s = *a;
+  s.h = kHeads;
+  s.q = ws + pl.q_off;
+  s.o = ws + pl.o_off;
+  s.sink = reinterpret_cast<float*>(ws + pl.sink_off);
+  s.lse = a->lse != nullptr ? reinterpret_cast<float*>(ws + pl.lse_off) : nullptr;
+  const int64_t bm = a->b * a->m;
+  s.sq[0] = a->m * kHeads * kDim;
+  s.sq[1] = kHeads * kDim;
+  s.sq[2] = kDim;
+  s.sq[3] = 1;
+  for (int i = 0; i < 4; ++i) s.so[i] = s.sq[i];
+  s.slse[0] = a->m * kHeads;
+  s.slse[1] = kHeads;
+  s.slse[2] = 1;
+  s.workspace_bytes = plan_bytes;
+  if (what == Launch::kPlanOnly) return forward16(&s, stream, events, launched, what);
+  PadParams pp{};
+  pp.q = static_cast<const __bf16*>(a->q);
+  pp.sink = a->sink;
+  pp.qp = static_cast<__bf16*>(const_cast<void*>(s.q));
+  pp.sinkp = const_cast<float*>(s.sink);
+  pp.op = static_cast<const __bf16*>(s.o);
+  pp.lsep = s.lse;
+  pp.o = static_cast<__bf16*>(a->o);
+  pp.lse = a->lse;
+  pp.m = a->m;
+  pp.h = a->h;
+  pp.sq_b = a->sq[0];
+  pp.sq_m = a->sq[1];
+  pp.sq_h = a->sq[2];
+  pp.so_b = a->so[0];
+  pp.so_m = a->so[1];
+  pp.so_h = a->so[2];
+  pp.sl_b = a->slse[0];
+  pp.sl_m = a->slse[1];
+  pp.sl_h = a->slse[2];
+  pp.rows = bm * kHeads;
+  hipLaunchKernelGGL(sa_pad_heads_kernel, dim3(unsigned((pp.rows * (kDim / 8) + 255) / 256)),
+                     dim3(256), 0, stream, pp);
+  if (hipGetLastError() != hipSuccess) return SA_EHIP;
+  const int frc = forward16(&s, stream, events, launched, what);
+  if (frc != SA_OK) return frc;
+  pp.rows = bm * a->h;
+  hipLaunchKernelGGL(sa_unpad_heads_kernel, dim3(unsigned((pp.rows * (kDim / 8) + 255) / 256)),
+                     dim3(256), 0, stream, pp);
+  return hipGetLastError() == hipSuccess ? SA_OK : SA_EHIP;
+}
+
+int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_t* launched,
+              Launch what) {
   const int rc = sa::validate(a);
   if (rc != SA_OK) return rc;
   if (a->b == 0 || a->m == 0) return SA_OK;

@@ -245,7 +245,8 @@ def sparse_attn_plan(q, kv, topk_idxs):
 def sparse_attn(q, kv, attn_sink, topk_idxs, scale, plan=None):
     """
     Args:
-        q:          [b, m, h, d]   bf16   (h = 16, d = 512)
+        q:          [b, m, h, d]   bf16   (d = 512; h = 1, 2, 4, 8 or a multiple of
+                                           16; the contest's model has h = 16)
         kv:         [b, kv_len, d] bf16   (K and V share rows)
         attn_sink:  [h]            fp32
         topk_idxs:  [b, m, topk]   int32  (-1 = padding slot)

@@ -148,7 +148,7 @@ def test_forward_events_rejects_bad_args_without_device_work(libs):
                                       ctypes.POINTER(ctypes.c_uint32)]
     launched = ctypes.c_uint32(7)
     a = good_args()
-    a.h = 8
+    a.h = 12
     assert hip.sa_forward_events(ctypes.byref(a), None, None, ctypes.byref(launched)) == \
         SA_EUNSUPPORTED
     assert launched.value == 0
@@ -209,7 +209,8 @@ def test_forward_rejects_null_args(libs):
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("h", 8, SA_EUNSUPPORTED), ("d", 256, SA_EUNSUPPORTED),
+    ("h", 12, SA_EUNSUPPORTED), ("h", 0, SA_EUNSUPPORTED), ("h", 24, SA_EUNSUPPORTED),
+    ("h", 3, SA_EUNSUPPORTED), ("d", 256, SA_EUNSUPPORTED),
     ("b", -1, SA_EINVAL), ("topk", -3, SA_EINVAL), ("kv_len", -1, SA_EINVAL),
     ("q", 0, SA_EINVAL), ("o", 0, SA_EINVAL), ("sink", 0, SA_EINVAL),
     ("idx", 0, SA_EINVAL), ("kv", 0, SA_EINVAL),
@@ -435,3 +436,25 @@ def test_merge_optional_and_empty(libs):
     a = good_merge(b=0)
     a.o = None                          # empty output: nothing to check or run
     assert hip.sa_merge(ctypes.byref(a), None) == SA_OK
+
+
+@pytest.mark.parametrize("h", [1, 2, 4, 8, 16, 32, 48, 64])
+def test_supported_head_counts_validate(libs, h):
+    """Powers of two up to 8 (padded to 16 in the workspace) and multiples of
+    16 (16-head slices) pass the host checks; the workspace of a call with
+    fewer than 16 heads holds a 16-head copy of q and o beyond the plan."""
+    hip, host = libs
+    a = good_args()
+    a.h = h
+    a.sq[:] = [a.m * h * 512, h * 512, 512, 1]
+    a.so[:] = list(a.sq)
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_OK
+    ws = ctypes.c_int64(0)
+    assert host.sa_host_workspace_bytes(ctypes.byref(a), 256, ctypes.byref(ws)) == SA_OK
+    a16 = good_args()
+    ws16 = ctypes.c_int64(0)
+    assert host.sa_host_workspace_bytes(ctypes.byref(a16), 256, ctypes.byref(ws16)) == SA_OK
+    if h < 16:
+        assert ws.value >= ws16.value + 2 * a.b * a.m * 16 * 512 * 2
+    else:
+        assert ws.value == ws16.value
