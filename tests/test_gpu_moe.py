@@ -111,9 +111,11 @@ def test_renormalize(gpu_sa, shape):
 
 @pytest.mark.parametrize("flags", [1, 2, 4], ids=["large", "small", "big"])
 @pytest.mark.parametrize("shape", [(64, 2048, 1024, 8, 2), (512, 1024, 512, 64, 6),
-                                   (200, 256, 128, 4, 2)])
+                                   (200, 256, 128, 4, 2), (300, 1280, 384, 4, 3)])
 def test_forced_tiles(gpu_sa, shape, flags):
-    """Every GEMM kernel on the same inputs, whichever the library would pick."""
+    """Every GEMM kernel on the same inputs, whichever the library would pick
+    (the last shape: odd column-tile counts, 3 for gate-up and 5 for down, so
+    the two column halves of the XCD work split differ in size)."""
     M, K, N, E, topk = shape
     hidden, w1, w2, score = make_inputs(M, K, N, E, seed=4)
     out = op(hidden, w1, w2, score, topk, flags=flags)
@@ -142,7 +144,7 @@ def test_every_token_on_one_expert(gpu_sa):
 
 
 @pytest.mark.parametrize("shape", [(1500, 512, 256, 8, 2), (700, 1024, 512, 4, 3),
-                                   (2048, 2048, 1024, 8, 2)])
+                                   (2048, 2048, 1024, 8, 2), (700, 1280, 384, 4, 3)])
 def test_big_tiles_equal_large_tiles(gpu_sa, shape):
     """256-pair tiles (8 waves, 32-wide K stages) and 128-pair tiles (4 waves,
     64-wide stages) run the same MFMA sequence per output element, so they
