@@ -713,6 +713,50 @@ def bench_contest(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     return recs
 
 
+# Library GEMMs (torch.bmm, which ROCm routes to hipBLASLt) on dense,
+# contiguous bf16 operands: what a tuned MFMA GEMM sustains on this GPU at
+# its sustained clock. The square products are the best case; the batched
+# ones are fused_moe's per-expert GEMMs at its largest prefill workload
+# (M=4096, E=64, topk=6: 384 pairs per expert on average, K=2048, N=1024).
+GEMM_CEILING_SHAPES = [  # label, batch, m, k, n
+    ("square 4096", 1, 4096, 4096, 4096),
+    ("square 8192", 1, 8192, 8192, 8192),
+    ("moe gate-up per expert", 64, 384, 2048, 2048),
+    ("moe down per expert", 64, 384, 1024, 2048),
+]
+
+
+def gemm_ceiling(steps, warmup):
+    """Time each GEMM_CEILING_SHAPES product: `warmup` untimed calls, then
+    `steps` calls between two events on the current stream."""
+    recs = []
+    for label, bt, m, k, n in GEMM_CEILING_SHAPES:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = torch.randn(bt, m, k, dtype=torch.bfloat16, device="cuda", generator=g)
+        b = torch.randn(bt, k, n, dtype=torch.bfloat16, device="cuda", generator=g)
+        out = torch.empty(bt, m, n, dtype=torch.bfloat16, device="cuda")
+        for _ in range(warmup):
+            torch.bmm(a, b, out=out)
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            torch.bmm(a, b, out=out)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        flops = 2.0 * bt * m * k * n
+        recs.append({"op": "torch.bmm (hipBLASLt)", "workload": label,
+                     "shape": {"batch": bt, "m": m, "k": k, "n": n},
+                     "us_per_call": round(us, 2), "tflops": round(flops / us / 1e6, 1),
+                     "frac_of_peak": round(flops / us / 1e6 / PEAK_MFMA_TFLOPS, 4),
+                     "dtype": "bf16", "data": "synthetic (seeded device randn)"})
+        del a, b, out
+        torch.cuda.empty_cache()
+    return recs
+
+
 def copy_calibration(mib=1024, reps=5):
     """A plain device-to-device copy of `mib` MiB, `reps` times: under
     rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE per dispatch scale the
@@ -749,6 +793,9 @@ def main():
                     help="with --moe: only workload i (0..7) of track-03/workloads.py")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy of known size (PMC byte scaling)")
+    ap.add_argument("--gemm-ceiling", action="store_true",
+                    help="time library bf16 GEMMs (torch.bmm -> hipBLASLt) instead: the MFMA "
+                         "rate a tuned GEMM sustains here")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (sparse_attn has no multi-GPU "
@@ -759,6 +806,10 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.gemm_ceiling:
+        for rec in gemm_ceiling(args.steps, args.warmup):
+            print(json.dumps(rec), flush=True)
         return
     if args.sinkhorn:
         for rec in bench_sinkhorn(args.steps, args.warmup, args.sets, not args.no_cpu,

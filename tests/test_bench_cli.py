@@ -109,3 +109,13 @@ def test_roofline_record_checks_provenance(monkeypatch):
     assert abs(r["profile"]["live_over_profile"] - 1.0) < 1e-9
     r = bench.roofline("causal_prefill", flops, 1.0, {"tile": 0.2}, {"tile": 1.0}, 150.0)
     assert r["frac"] is None and "exceeds" in r["frac_note"]
+
+
+def test_gemm_ceiling_shapes_follow_the_moe_workload():
+    # the batched library GEMMs are fused_moe's per-expert products at its
+    # largest prefill workload: E experts of M * topk / E pairs each
+    label, M, K, N, E, topk = bench.MOE_WORKLOADS[7]
+    assert (label, M, E, topk) == ("prefill", 4096, 64, 6)
+    shapes = {lab: (bt, m, k, n) for lab, bt, m, k, n in bench.GEMM_CEILING_SHAPES}
+    assert shapes["moe gate-up per expert"] == (E, M * topk // E, K, 2 * N)
+    assert shapes["moe down per expert"] == (E, M * topk // E, N, K)
