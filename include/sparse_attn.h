@@ -93,7 +93,8 @@ typedef struct sa_args {
   int64_t sidx[3];        /* strides of idx */
   int64_t so[4];          /* strides of o   */
   float scale;            /* softmax scale, e.g. d**-0.5 */
-  void* workspace;        /* device scratch: tile row unions, split partials */
+  void* workspace;        /* device scratch: tile row unions, split partials;
+                             16-byte aligned (ABI version 7) */
   size_t workspace_bytes;
   int32_t* err_word;      /* int32, nullable; set to 1 when a bad index is seen
                              (a system-scope store, never cleared by the library:

@@ -116,6 +116,7 @@ inline int validate(const sa_args* a) {
   // 16-byte row loads and stores
   if (!aligned16(a->q) || !aligned16(a->o)) return SA_EINVAL;
   if (a->kv_len > 0 && !aligned16(a->kv)) return SA_EINVAL;
+  if (a->workspace != nullptr && !aligned16(a->workspace)) return SA_EINVAL;  // vector loads
   for (int i = 0; i < 3; ++i)
     if (a->sq[i] % 8 != 0 || a->so[i] % 8 != 0) return SA_EINVAL;
   for (int i = 0; i < 2; ++i)

@@ -216,7 +216,7 @@ def test_forward_rejects_null_args(libs):
     ("idx", 0, SA_EINVAL), ("kv", 0, SA_EINVAL),
     ("q", 0x10008, SA_EINVAL), ("o", 0x50002, SA_EINVAL), ("kv", 0x20004, SA_EINVAL),
     ("scale", float("nan"), SA_EINVAL), ("flags", 32, SA_EINVAL), ("flags", 8 | 16, SA_EINVAL),
-    ("flags", 1 << 31, SA_EINVAL),
+    ("flags", 1 << 31, SA_EINVAL), ("workspace", 0x70008, SA_EINVAL),
 ])
 def test_forward_argument_errors(libs, field, value, code):
     hip, host = libs
