@@ -480,8 +480,7 @@ struct GemmParams {
   int topk;
   int col_tiles;         // output-column tiles per pair tile
   int ct_per_wg;         // column tiles one work-group runs (fm_stream_kernel)
-  int spread;            // large/big tiles, at most one work item per CU: b -> (b / col_tiles,
-                         // b % col_tiles) instead of the XCD grid of xcd_item
+  int xcd_grid;          // large/big tiles: the 2 x 4 XCD grid of xcd_item
   // GEMM 2 with topk <= 2 (fm_stream_kernel): add each pair's bf16 row into
   // the token's output row instead of writing yw (null: write yw)
   __bf16* fsum;
@@ -501,19 +500,21 @@ __device__ __forceinline__ void add_bf16x2(__bf16* out, __bf16 a0, __bf16 a1) {
 
 // Work item (pair tile, column tile) of a large or big GEMM work-group.
 // Work-group b runs on XCD b % 8 (dispatch is round-robin over the XCDs, in
-// order of b). The XCDs form a 2 x 4 grid: XCD x takes column tiles of half
-// x % 2 of every pair tile in its contiguous quarter x / 2 of the tile table,
-// pair tile by pair tile. A pair tile's gathered A rows are then read into two
-// XCDs' L2 instead of col_tiles of them, and the pair tiles of one expert
-// (adjacent in the table) mostly share their weight rows within one L2.
-// Measured against b -> (b / col_tiles, b % col_tiles), which puts column
-// tile c of every pair tile on XCD c % 8, at K = 2048, N = 1024: 5 % faster
-// at M = 4096, E = 64, topk = 6; 1-4 % at M = 512-3072; 8 % slower at M =
-// 8192, E = 8, topk = 2, where each expert has 8 pair tiles. Whole column
-// tiles on each XCD (an 8 x 1 grid) gain 10 % at M = 4096, E = 64 but lose
-// 15 % at M = 4096, E = 8. When every item has a CU of its own (p.spread)
-// there is no reuse over time to arrange, and b -> (b / col_tiles, b %
-// col_tiles) is kept (2 us faster at M = 512, E = 8, topk = 2, 64 items).
+// order of b). Plainly, b -> (b / col_tiles, b % col_tiles): column tile c of
+// every pair tile runs on XCD c % 8, so a weight tile is read into one L2 and
+// shared there by the pair tiles of its expert, while every pair tile's
+// gathered A rows are read into col_tiles L2s. With p.xcd_grid the XCDs form
+// a 2 x 4 grid instead: XCD x takes the column tiles of half x % 2 of every
+// pair tile in its contiguous quarter x / 2 of the tile table, pair tile by
+// pair tile, so a pair tile's A rows go to two L2s, and an expert's pair
+// tiles (adjacent in the table) still share its weight rows in one L2.
+// The host sets xcd_grid when experts average fewer than two pair tiles and
+// the items outnumber the CUs. Measured at K = 2048, N = 1024 (gate-up +
+// down): M = 4096, E = 64, topk = 6 (1.5 pair tiles per expert) 5-10 %
+// faster; M = 512-3072 at E = 64, 1-7 %; but M = 4096, E = 8, topk = 2 (4
+// pair tiles per expert) 20 % slower with one set of routings and level with
+// another, and M = 8192, E = 8 8 % slower. Whole column tiles on each XCD
+// (an 8 x 1 grid) gained 10 % at M = 4096, E = 64 and lost 15 % at E = 8.
 // False: no item for this work-group.
 constexpr int kXcds = 8;
 constexpr int kXcdColGroups = 2;
@@ -522,7 +523,7 @@ constexpr int kXcdTileGroups = kXcds / kXcdColGroups;
 __device__ __forceinline__ bool xcd_item(const GemmParams& p, int& tile, int& ct) {
   const int nt = p.tiles[0];
   const int b = int(blockIdx.x);
-  if (p.spread) {
+  if (!p.xcd_grid) {
     tile = b / p.col_tiles;
     ct = b % p.col_tiles;
     return tile < nt;
@@ -1395,8 +1396,11 @@ int forward(const fm_args* a, hipStream_t stream, void* const* events, uint32_t*
     g2.fsum_stride = a->s_out;
   }
   g1.ct_per_wg = g2.ct_per_wg = 1;
-  for (GemmParams* g : {&g1, &g2})  // MI355X: 256 CUs, one large or big work-group each
-    g->spread = pl.large && pl.max_tiles * g->col_tiles <= 256;
+  // (MI355X: 256 CUs, one large or big work-group each)
+  const double pairs_per_expert = double(pl.P) / double(a->E);
+  for (GemmParams* g : {&g1, &g2})
+    g->xcd_grid = pl.large && pairs_per_expert < 2.0 * pl.tile_rows &&
+                  pl.max_tiles * g->col_tiles > 256;
   if (streamed) {
     // a streaming work-group runs several column tiles in one pipeline, so its
     // start (tile table -> pair list -> first DMA) is paid once per
