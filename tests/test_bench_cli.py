@@ -119,3 +119,20 @@ def test_gemm_ceiling_shapes_follow_the_moe_workload():
     shapes = {lab: (bt, m, k, n) for lab, bt, m, k, n in bench.GEMM_CEILING_SHAPES}
     assert shapes["moe gate-up per expert"] == (E, M * topk // E, K, 2 * N)
     assert shapes["moe down per expert"] == (E, M * topk // E, N, K)
+
+
+def test_torch_eager_baseline_is_the_reference_oracle():
+    # the contest bench's denominator (the reference's own metric) computes
+    # what the oracle computes, in the same order: on CPU tensors the two
+    # agree bit for bit
+    from oracle.sparse_attn_ref import sparse_attn_ref
+    g = torch.Generator().manual_seed(3)
+    b, m, h, d, kv_len, topk = 2, 3, 16, 512, 40, 7
+    q = torch.randn(b, m, h, d, generator=g).to(torch.bfloat16)
+    kv = torch.randn(b, kv_len, d, generator=g).to(torch.bfloat16)
+    sink = torch.randn(h, generator=g)
+    idx = torch.randint(0, kv_len, (b, m, topk), generator=g, dtype=torch.int32)
+    got = bench.torch_eager_attn(q, kv, sink, idx, 0.044)
+    want = sparse_attn_ref(q, kv, sink, idx, 0.044)
+    assert got.dtype == torch.bfloat16 and got.shape == (b, m, h, d)
+    assert torch.equal(got, want)
