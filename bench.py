@@ -362,6 +362,11 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     ms_rr_plain, ms_planned, rounds = time_alternating(
         submission.sparse_attn, sets, scale, steps, warmup, plans)
     del plans
+    # the reference's own metric: its torch oracle, eager on this GPU, over this call
+    masked = bool((idx == -1).any())
+    ms_eager = time_calls(lambda *a: torch_eager_attn(*a, masked=masked), sets, scale,
+                          min(steps, 5), min(warmup, 2))
+    torch.cuda.empty_cache()
     t = ms * 1e-3
     tflops = flops / t / 1e12
     gbps = gathered / t / 1e9
@@ -395,6 +400,13 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                     "note": (f"index plan made before the timed calls and reused; timed in "
                              f"{rounds} alternating blocks of plain and planned calls "
                              f"(plain_us_per_call: the plain calls of those blocks)")},
+        "torch_eager": {"us_per_call": round(ms_eager * 1e3, 2),
+                        "speedup": round(ms_eager / ms, 2),
+                        "note": ("the reference's own metric (track-01/bench.py:26-50): its "
+                                 "torch oracle as eager torch on this GPU (torch_eager_attn"
+                                 + (", -1 slots masked" if masked else "") + ") over this "
+                                 "call; it publishes 1.12x for its Triton hip backend, "
+                                 "3.99x at best, on its contest shapes (README.md:14-15)")},
     }
     rec["cpu_baseline"] = cpu_baseline(cpu_inputs) if with_cpu else None
     del sets
@@ -670,18 +682,27 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
     return recs
 
 
-def torch_eager_attn(q, kv, attn_sink, topk_idxs, scale):
+def torch_eager_attn(q, kv, attn_sink, topk_idxs, scale, masked=False):
     """The denominator of the reference's own benchmark: its PyTorch oracle
     (track-01/reference/reference.py:24-40), which track-01/bench.py:26-47
     times on the same device as the kernel. The same torch operations in the
     same order and precision (row gather, fp32 einsums, the sink appended as
     a logit, softmax over topk + 1, cast to q's dtype), here on the GPU, for
-    timing only: parity is checked against oracle/ in tests/."""
+    timing only: parity is checked against oracle/ in tests/. masked: the
+    indices hold -1 slots, which the frozen oracle's gather rejects; they
+    gather row 0 and take a -inf logit (the rule of track-01/submission.py:
+    313-322), two more operations."""
     b, m, h, d = q.shape
     t = topk_idxs.shape[-1]
-    rows = torch.gather(kv, 1, topk_idxs.long().reshape(b, m * t, 1).expand(b, m * t, d))
+    idx = topk_idxs.long()
+    if masked:
+        valid = idx >= 0
+        idx = idx.clamp(min=0)
+    rows = torch.gather(kv, 1, idx.reshape(b, m * t, 1).expand(b, m * t, d))
     rows = rows.reshape(b, m, t, d)
     logits = torch.einsum("bmhd,bmtd->bmht", q.float(), rows.float()) * scale
+    if masked:
+        logits = logits.masked_fill(~valid[:, :, None, :], float("-inf"))
     logits = torch.cat([logits, attn_sink.view(1, 1, h, 1).expand(b, m, h, 1)], dim=-1)
     w = torch.softmax(logits, dim=-1)[..., :t]
     return torch.einsum("bmht,bmtd->bmhd", w, rows.float()).to(q.dtype)

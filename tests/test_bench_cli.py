@@ -136,3 +136,21 @@ def test_torch_eager_baseline_is_the_reference_oracle():
     want = sparse_attn_ref(q, kv, sink, idx, 0.044)
     assert got.dtype == torch.bfloat16 and got.shape == (b, m, h, d)
     assert torch.equal(got, want)
+
+
+def test_torch_eager_baseline_masks_padding_like_the_oracle():
+    # with -1 slots (causal prefill's padding) the baseline masks them as the
+    # oracle does; an all -1 query gives o = 0
+    from oracle.sparse_attn_ref import sparse_attn_ref
+    g = torch.Generator().manual_seed(4)
+    b, m, h, d, kv_len, topk = 1, 4, 16, 512, 30, 9
+    q = torch.randn(b, m, h, d, generator=g).to(torch.bfloat16)
+    kv = torch.randn(b, kv_len, d, generator=g).to(torch.bfloat16)
+    sink = torch.randn(h, generator=g)
+    idx = torch.randint(0, kv_len, (b, m, topk), generator=g, dtype=torch.int32)
+    idx[0, 1, 5:] = -1
+    idx[0, 3, :] = -1
+    got = bench.torch_eager_attn(q, kv, sink, idx, 0.044, masked=True)
+    want = sparse_attn_ref(q, kv, sink, idx, 0.044)
+    assert torch.equal(got, want)
+    assert not bool(got[0, 3].any())
