@@ -422,8 +422,29 @@ HC_WORKLOADS = [  # track-02/workloads.py:19-24: name, decode (b, s), share, pre
 ]
 
 
+def torch_eager_sinkhorn(mixes, hc_scale, hc_base, hc_mult=4, iters=20, eps=1e-6):
+    """The denominator of track 02's own benchmark: its torch oracle
+    (track-02/reference/reference.py:33-51), timed by track-02/bench.py:19-64
+    on the same device as the kernel; the same torch operations in the same
+    order, eager on the GPU, for timing only (parity: tests/ against oracle/)."""
+    b, s, _ = mixes.shape
+    hc = hc_mult
+    pre = torch.sigmoid(mixes[..., :hc] * hc_scale[0] + hc_base[:hc]) + eps
+    post = 2 * torch.sigmoid(mixes[..., hc:2 * hc] * hc_scale[1] + hc_base[hc:2 * hc])
+    comb = mixes[..., 2 * hc:].reshape(b, s, hc, hc) * hc_scale[2] + hc_base[2 * hc:].reshape(hc, hc)
+    comb = torch.softmax(comb, dim=-1) + eps
+    comb = comb / (comb.sum(dim=-2, keepdim=True) + eps)
+    for _ in range(iters - 1):
+        comb = comb / (comb.sum(dim=-1, keepdim=True) + eps)
+        comb = comb / (comb.sum(dim=-2, keepdim=True) + eps)
+    return pre, post, comb
+
+
 def bench_sinkhorn(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
-    """One record per track-02 scenario (see the module docstring)."""
+    """One record per track-02 scenario (see the module docstring), each with
+    track 02's own metric: the torch oracle's frequency-weighted time over the
+    kernel's on the same GPU (torch_eager_sinkhorn); a last record holds its
+    geometric mean over the scenarios (track-02/bench.py:55-64)."""
     from hc_sinkhorn import FLAG_LANES1, FLAG_LANES16, hc_split_sinkhorn
     recs = []
 
@@ -480,8 +501,17 @@ def bench_sinkhorn(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                           "us_lanes16": round(us_per_call(sets, FLAG_LANES16), 2),
                           "us_lanes1": round(us_per_call(sets, FLAG_LANES1), 2),
                           "us_capi": round(us_capi(sets), 2)}
+            # last: its many temporaries would slow the host-bound calls above
+            eager = time_calls(lambda m, sc, bs, _u, _s: torch_eager_sinkhorn(m, sc, bs),
+                               [(m, sc, bs, None) for m, sc, bs in sets], None, steps,
+                               warmup) * 1e3
+            rec[stage]["torch_eager_us_per_call"] = round(eager, 2)
         rec["weighted_us"] = round(dshare * rec["decode"]["us_per_call"] +
                                    pshare * rec["prefill"]["us_per_call"], 3)
+        eager_w = (dshare * rec["decode"]["torch_eager_us_per_call"] +
+                   pshare * rec["prefill"]["torch_eager_us_per_call"])
+        rec["torch_eager_weighted_us"] = round(eager_w, 3)
+        rec["speedup_vs_torch_eager"] = round(eager_w / rec["weighted_us"], 2)
         n = rec["prefill"]["tokens"]
         hbm = n * 192 + 27 * 4
         ach = hbm / (rec["prefill"]["us_per_call"] * 1e-6) / 1e9
@@ -507,6 +537,14 @@ def bench_sinkhorn(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                                    "unit": "us/call", "cores": 1, "kind": "port",
                                    "sample": "whole call, NumPy float32 restatement, median of 3"}
         recs.append(rec)
+    sp = [r["speedup_vs_torch_eager"] for r in recs]
+    recs.append({"op": "hc_split_sinkhorn", "scenario": "geomean",
+                 "speedup_vs_torch_eager_geomean":
+                     round(math.exp(sum(math.log(x) for x in sp) / len(sp)), 2),
+                 "scenarios": len(sp),
+                 "note": "track 02's summary figure (track-02/bench.py:62-64): the geometric "
+                         "mean over its four scenarios of the torch oracle's frequency-"
+                         "weighted time over the kernel's, on one device"})
     return recs
 
 
@@ -605,6 +643,28 @@ def moe_cpu_baseline(hidden, w1, w2, score, topk, target_s=3.0, runs=3):
                        f"(oracle/fused_moe_ref.py, routed tokens only), {threads} threads")}
 
 
+def torch_eager_moe(hidden, w1, w2, score, topk, renormalize=False):
+    """Track 03's torch oracle (track-03/reference/reference.py:10-35), eager on
+    the GPU: routing by fp32 softmax and top-k, then every expert's two dense
+    products over all M tokens, weighted by the token's routing weight (zero
+    for tokens not routed there). Track 03 ships no bench; this is the
+    denominator its sibling tracks' benches use (track-01/bench.py:26-50,
+    track-02/bench.py:19-64). Timing only (parity: tests/ against oracle/)."""
+    M, K = hidden.shape
+    E, N = w1.shape[0], w2.shape[-1]
+    w, ids = score.softmax(dim=-1, dtype=torch.float32).topk(topk, dim=-1)
+    if renormalize:
+        w = w / w.sum(dim=-1, keepdim=True)
+    w = w.to(hidden.dtype)
+    out = torch.zeros(M, K, device=hidden.device, dtype=hidden.dtype)
+    for e in range(E):
+        tw = (w * (ids == e)).sum(dim=-1, keepdim=True)
+        x = torch.nn.functional.linear(hidden, w1[e])
+        x = x[:, N:] * torch.nn.functional.silu(x[:, :N])
+        out += torch.nn.functional.linear(x, w2[e]) * tw
+    return out
+
+
 def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
     """One record per track-03 workload: µs/call of the drop-in
     (submission.fused_moe), algorithmic TFLOP/s (6 N K flop per routed
@@ -626,6 +686,8 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
             settle(fn, tsets, None, settle_s)
             first = False
         ms = time_calls(fn, tsets, None, steps, warmup)
+        ms_eager = time_calls(lambda h, a1, a2, sc, _s: torch_eager_moe(h, a1, a2, sc, topk),
+                              tsets, None, min(steps, 5), min(warmup, 2))
         times = moe_kernel_times(sets, topk, steps, warmup)
         hidden, w1, w2, score = sets[0]
         ids, _ = route(score.cpu(), topk)
@@ -673,12 +735,25 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
                "config": {"workload": f"fused_moe {label} M={M} K={K} N={N} E={E} topk={topk}",
                           "pairs": P, "experts_used": used, "flops_alg": flops,
                           "compulsory_bytes": wbytes + io, "input_sets_rotated": nsets},
-               "roofline": roof, "vs_baseline": None}
+               "roofline": roof, "vs_baseline": None,
+               "torch_eager": {"us_per_call": round(ms_eager * 1e3, 2),
+                               "speedup": round(ms_eager / ms, 2),
+                               "note": "track 03's torch oracle as eager torch on this GPU "
+                                       "(torch_eager_moe) over this call"}}
         hc = [x.cpu() for x in sets[0]] if with_cpu else None
         del sets, tsets, hidden, w1, w2, score
         torch.cuda.empty_cache()
         rec["cpu_baseline"] = moe_cpu_baseline(*hc, topk) if with_cpu else None
         recs.append(rec)
+    if only is None:
+        sp = [r["torch_eager"]["speedup"] for r in recs]
+        recs.append({"metric": "fused_moe speedup over the torch oracle, geometric mean",
+                     "speedup_vs_torch_eager_geomean":
+                         round(math.exp(sum(math.log(x) for x in sp) / len(sp)), 2),
+                     "workloads": len(sp),
+                     "note": "the geometric mean over track 03's eight workloads of the torch "
+                             "oracle's time over the call's, on one device (the summary "
+                             "figure of track-01/bench.py:49-50 and track-02/bench.py:62-64)"})
     return recs
 
 

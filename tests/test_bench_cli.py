@@ -154,3 +154,33 @@ def test_torch_eager_baseline_masks_padding_like_the_oracle():
     want = sparse_attn_ref(q, kv, sink, idx, 0.044)
     assert torch.equal(got, want)
     assert not bool(got[0, 3].any())
+
+
+def test_torch_eager_moe_is_the_track03_oracle():
+    # the MoE denominator runs the oracle's dense form (every expert over every
+    # token, weight 0 where not routed); on CPU tensors it matches oracle/,
+    # which runs the routed tokens only, bit for bit
+    from oracle.fused_moe_ref import fused_moe_ref
+    g = torch.Generator().manual_seed(5)
+    M, K, N, E, topk = 12, 256, 128, 4, 2
+    hidden = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w1 = (torch.randn(E, 2 * N, K, generator=g) * 0.02).to(torch.bfloat16)
+    w2 = (torch.randn(E, K, N, generator=g) * 0.02).to(torch.bfloat16)
+    score = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    for renorm in (False, True):
+        got = bench.torch_eager_moe(hidden, w1, w2, score, topk, renorm)
+        want = fused_moe_ref(hidden, w1, w2, score, topk, renorm)
+        assert got.dtype == torch.bfloat16 and got.shape == (M, K)
+        assert torch.equal(got, want)
+
+
+def test_torch_eager_sinkhorn_is_the_track02_oracle():
+    from oracle.hc_sinkhorn_ref import hc_split_sinkhorn_np
+    g = torch.Generator().manual_seed(6)
+    mixes = torch.randn(3, 5, 24, generator=g)
+    sc, bs = torch.randn(3, generator=g), torch.randn(24, generator=g)
+    got = bench.torch_eager_sinkhorn(mixes, sc, bs)
+    want = hc_split_sinkhorn_np(mixes.numpy(), sc.numpy(), bs.numpy())
+    for a, b in zip(got, want):
+        assert tuple(a.shape) == b.shape
+        assert torch.allclose(a, torch.from_numpy(b), rtol=1e-5, atol=1e-6)
