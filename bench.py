@@ -80,6 +80,10 @@ import sa_workloads as wl  # noqa: E402
 METRIC = ("sparse_attn µs/call, TFLOP/s + gathered-KV GB/s (% roofline) "
           "at m4096 topk2048")
 PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+# Time each op's torch oracle as eager torch on the GPU beside it (the
+# reference's own speedup metric); --no-eager turns it off (profiling runs,
+# whose traces would otherwise hold the oracle's many small launches).
+EAGER = True
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 H, D = wl.NUM_HEADS, wl.HEAD_DIM
 KERNEL_NAMES = {"index": "sa_tile_index_kernel", "tile": "sa_fwd_tile_kernel",
@@ -365,7 +369,7 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
     # the reference's own metric: its torch oracle, eager on this GPU, over this call
     masked = bool((idx == -1).any())
     ms_eager = time_calls(lambda *a: torch_eager_attn(*a, masked=masked), sets, scale,
-                          min(steps, 5), min(warmup, 2))
+                          min(steps, 5), min(warmup, 2)) if EAGER else None
     torch.cuda.empty_cache()
     t = ms * 1e-3
     tflops = flops / t / 1e12
@@ -406,7 +410,8 @@ def bench_config(name, steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                                  "torch oracle as eager torch on this GPU (torch_eager_attn"
                                  + (", -1 slots masked" if masked else "") + ") over this "
                                  "call; it publishes 1.12x for its Triton hip backend, "
-                                 "3.99x at best, on its contest shapes (README.md:14-15)")},
+                                 "3.99x at best, on its contest shapes (README.md:14-15)")}
+                       if ms_eager is not None else None,
     }
     rec["cpu_baseline"] = cpu_baseline(cpu_inputs) if with_cpu else None
     del sets
@@ -502,16 +507,18 @@ def bench_sinkhorn(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                           "us_lanes1": round(us_per_call(sets, FLAG_LANES1), 2),
                           "us_capi": round(us_capi(sets), 2)}
             # last: its many temporaries would slow the host-bound calls above
-            eager = time_calls(lambda m, sc, bs, _u, _s: torch_eager_sinkhorn(m, sc, bs),
-                               [(m, sc, bs, None) for m, sc, bs in sets], None, steps,
-                               warmup) * 1e3
-            rec[stage]["torch_eager_us_per_call"] = round(eager, 2)
+            if EAGER:
+                eager = time_calls(lambda m, sc, bs, _u, _s: torch_eager_sinkhorn(m, sc, bs),
+                                   [(m, sc, bs, None) for m, sc, bs in sets], None, steps,
+                                   warmup) * 1e3
+                rec[stage]["torch_eager_us_per_call"] = round(eager, 2)
         rec["weighted_us"] = round(dshare * rec["decode"]["us_per_call"] +
                                    pshare * rec["prefill"]["us_per_call"], 3)
-        eager_w = (dshare * rec["decode"]["torch_eager_us_per_call"] +
-                   pshare * rec["prefill"]["torch_eager_us_per_call"])
-        rec["torch_eager_weighted_us"] = round(eager_w, 3)
-        rec["speedup_vs_torch_eager"] = round(eager_w / rec["weighted_us"], 2)
+        if EAGER:
+            eager_w = (dshare * rec["decode"]["torch_eager_us_per_call"] +
+                       pshare * rec["prefill"]["torch_eager_us_per_call"])
+            rec["torch_eager_weighted_us"] = round(eager_w, 3)
+            rec["speedup_vs_torch_eager"] = round(eager_w / rec["weighted_us"], 2)
         n = rec["prefill"]["tokens"]
         hbm = n * 192 + 27 * 4
         ach = hbm / (rec["prefill"]["us_per_call"] * 1e-6) / 1e9
@@ -537,6 +544,8 @@ def bench_sinkhorn(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                                    "unit": "us/call", "cores": 1, "kind": "port",
                                    "sample": "whole call, NumPy float32 restatement, median of 3"}
         recs.append(rec)
+    if not EAGER:
+        return recs
     sp = [r["speedup_vs_torch_eager"] for r in recs]
     recs.append({"op": "hc_split_sinkhorn", "scenario": "geomean",
                  "speedup_vs_torch_eager_geomean":
@@ -687,7 +696,7 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
             first = False
         ms = time_calls(fn, tsets, None, steps, warmup)
         ms_eager = time_calls(lambda h, a1, a2, sc, _s: torch_eager_moe(h, a1, a2, sc, topk),
-                              tsets, None, min(steps, 5), min(warmup, 2))
+                              tsets, None, min(steps, 5), min(warmup, 2)) if EAGER else None
         times = moe_kernel_times(sets, topk, steps, warmup)
         hidden, w1, w2, score = sets[0]
         ids, _ = route(score.cpu(), topk)
@@ -739,13 +748,14 @@ def bench_moe(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S, only=None):
                "torch_eager": {"us_per_call": round(ms_eager * 1e3, 2),
                                "speedup": round(ms_eager / ms, 2),
                                "note": "track 03's torch oracle as eager torch on this GPU "
-                                       "(torch_eager_moe) over this call"}}
+                                       "(torch_eager_moe) over this call"}
+                              if ms_eager is not None else None}
         hc = [x.cpu() for x in sets[0]] if with_cpu else None
         del sets, tsets, hidden, w1, w2, score
         torch.cuda.empty_cache()
         rec["cpu_baseline"] = moe_cpu_baseline(*hc, topk) if with_cpu else None
         recs.append(rec)
-    if only is None:
+    if only is None and EAGER:
         sp = [r["torch_eager"]["speedup"] for r in recs]
         recs.append({"metric": "fused_moe speedup over the torch oracle, geometric mean",
                      "speedup_vs_torch_eager_geomean":
@@ -813,7 +823,8 @@ def bench_contest(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
         ms = time_calls(submission.sparse_attn, sets, wl.SCALE, steps, warmup)
         # the reference's denominator, eager torch on this GPU (a few calls:
         # each materialises the gathered rows in fp32, up to 52 GB here)
-        ms_eager = time_calls(torch_eager_attn, sets, wl.SCALE, min(steps, 5), min(warmup, 2))
+        ms_eager = time_calls(torch_eager_attn, sets, wl.SCALE, min(steps, 5),
+                              min(warmup, 2)) if EAGER else None
         torch.cuda.empty_cache()
         n_valid = b * m * topk
         flops = 4.0 * H * D * n_valid
@@ -821,8 +832,8 @@ def bench_contest(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
                "shape": {"b": b, "m": m, "kv_len": kv_len, "topk": topk},
                "us_per_call": round(ms * 1e3, 2), "tflops": round(flops / (ms * 1e-3) / 1e12, 3),
                "gathered_kv_GBps": round(n_valid * D * 2 / (ms * 1e-3) / 1e9, 1),
-               "torch_eager_us_per_call": round(ms_eager * 1e3, 2),
-               "speedup_vs_torch_eager": round(ms_eager / ms, 2),
+               "torch_eager_us_per_call": round(ms_eager * 1e3, 2) if EAGER else None,
+               "speedup_vs_torch_eager": round(ms_eager / ms, 2) if EAGER else None,
                "dtype": "bf16", "data": "synthetic (seeded device randn, as make_inputs)"}
         if with_cpu:
             q, kv, sink, idx = (t.cpu() for t in sets[0])
@@ -832,6 +843,8 @@ def bench_contest(steps, warmup, nsets, with_cpu, settle_s=SETTLE_S):
         recs.append(rec)
         del sets
         torch.cuda.empty_cache()
+    if not EAGER:
+        return recs
     sp = [r["speedup_vs_torch_eager"] for r in recs]
     recs.append({"op": "sparse_attn", "workload": "geomean",
                  "speedup_vs_torch_eager_geomean":
@@ -911,6 +924,8 @@ def main():
     ap.add_argument("--sets", type=int, default=4)
     ap.add_argument("--all", action="store_true", help="also bench every config (stderr)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-eager", action="store_true",
+                    help="skip timing the torch oracles as eager torch on the GPU")
     ap.add_argument("--settle", type=float, default=SETTLE_S,
                     help="seconds of untimed calls before the timed loops (0 under a "
                          "counter-collecting profiler, which serialises every dispatch)")
@@ -928,6 +943,8 @@ def main():
                     help="time library bf16 GEMMs (torch.bmm -> hipBLASLt) instead: the MFMA "
                          "rate a tuned GEMM sustains here")
     args = ap.parse_args()
+    global EAGER
+    EAGER = not args.no_eager
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (sparse_attn has no multi-GPU "
               "path here); run with --gpus 1", file=sys.stderr)
