@@ -86,9 +86,9 @@ PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 EAGER = True
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 H, D = wl.NUM_HEADS, wl.HEAD_DIM
-KERNEL_NAMES = {"index": "sa_tile_index_kernel", "tile": "sa_fwd_tile_kernel",
-                "query": "sa_fwd_query_kernel", "combine": "sa_combine_kernel",
-                "wave": "sa_fwd_wave_kernel"}
+KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_order_kernel",
+                "tile": "sa_fwd_tile_kernel", "query": "sa_fwd_query_kernel",
+                "combine": "sa_combine_kernel", "wave": "sa_fwd_wave_kernel"}
 
 # HBM bytes per launch of the dominant kernel, from two rocprofv3 --pmc runs
 # (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) scaled by what the same
@@ -219,7 +219,7 @@ def kernel_times(sets, scale, steps, warmup):
     runs the shared tiles' slots and the per-query (or wave) kernel the
     others: the tile meta the index kernel leaves at workspace offset 0 (per
     tile: union size, mode, valid slots, overflow) tells them apart. Next to
-    the wave kernel the per-query launch only makes the tile order."""
+    the wave kernel the tile order has a launch of its own (order)."""
     import sa_capi
     lib = sa_capi.load()
     stream = torch.cuda.current_stream()

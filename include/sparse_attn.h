@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 7
+#define SA_ABI_VERSION 8
 
 /* Return codes. */
 enum {
@@ -205,16 +205,15 @@ int sa_plan_indices(const sa_args* a, void* hip_stream);
  * COMBINE when split; shared-row (tile) plans INDEX (unless SA_FLAG_PLANNED),
  * QUERY, TILE. In a tile plan the QUERY launch runs the queries of the tiles
  * the index kernel made per query, and makes the longest-first tile order
- * in its first work-group. (Version 5: the order no longer has a launch of
- * its own, so bit SA_KERNEL_ORDER is never set.) Version 6: unsplit plans
- * with topk <= 384 run their per-query
- * queries as WAVE instead, one wave per query; in a tile plan that makes
- * the tile order needs, QUERY is then a one-work-group launch that only
- * makes it.
+ * in its first work-group. (Version 5: the order no longer had a launch of
+ * its own.) Version 6: unsplit plans with topk <= 384 run their per-query
+ * queries as WAVE instead, one wave per query. Version 8: where QUERY would
+ * only make the tile order (such a plan, and sa_plan_indices), the order is
+ * ORDER, a one-work-group launch of its own: INDEX, ORDER, WAVE, TILE.
  */
 enum {
   SA_KERNEL_INDEX = 0,    /* row unions of shared-row tiles (tile plans)   */
-  SA_KERNEL_ORDER = 1,    /* not launched since version 5                  */
+  SA_KERNEL_ORDER = 1,    /* the tile order alone (version 8; see above)   */
   SA_KERNEL_TILE = 2,     /* shared-row tiles (tile plans)                 */
   SA_KERNEL_QUERY = 3,    /* per-query parts; in tile plans the per-query
                              tiles and the tile order                      */

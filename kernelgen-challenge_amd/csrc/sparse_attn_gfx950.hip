@@ -1276,55 +1276,123 @@ constexpr int kOrderPer = 8;  // tiles per thread per pass (their loads issued t
 constexpr int kOrderPlaceMax = 1024;
 // tiles whose keys the first pass keeps in LDS for the second (16-bit keys)
 constexpr int kOrderKeyCache = 16384;
+// With the keys cached, the 64-tile chunks whose per-query tiles are
+// counted for the second pass.
+constexpr int kOrderChunks = kOrderKeyCache / 64;
+// threads of the order's own launch (sa_order_kernel)
+constexpr int kOrderThreads = 1024;
 static_assert(kOrderKeys <= (1 << (31 - kOrderTileBits)), "keys fit the order entry");
 
 constexpr int kXcds = 8;  // MI355X: work-groups are dealt to the 8 XCDs round-robin
 
 struct OrderSmem {
   int pos[kOrderKeysPadded];
-  int wcount[kWaves];
+  int wcount[kOrderThreads / 64];
+  int zpre[kOrderChunks];  // per-query tiles in the 64-tile chunks before chunk c
   uint16_t key[kOrderKeyCache];
 };
 
-// The tile order, made by one work-group of kThreads threads.
+// Exclusive scan of n ints in LDS by one wave, in place; returns the total.
+__device__ __forceinline__ int wave_exclusive_scan(int* v, int n) {
+  const int lane = threadIdx.x & 63;
+  int carry = 0;
+  for (int c0 = 0; c0 < n; c0 += 64) {
+    const int i = c0 + lane;
+    const int x = i < n ? v[i] : 0;
+    int incl = x;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off);
+      if (lane >= off) incl += t;
+    }
+    if (i < n) v[i] = carry + incl - x;
+    carry += __shfl(incl, 63);
+  }
+  return carry;
+}
+
+// The tile order, made by one work-group of NT threads: work-group 0 of the
+// tile-plan per-query launch (NT = kThreads), or sa_order_kernel (NT =
+// kOrderThreads) where that launch would do nothing else.
+//  * Pass 1 reads every tile's key and counts the keys in LDS. With at most
+//    kOrderKeyCache tiles, the (union size, mode) pairs of kOrderLoad tiles
+//    per thread are loaded as 8-byte words, all issued before any is used,
+//    and the keys stay in LDS for pass 2.
+//  * The counts are scanned in descending key order.
+//  * Pass 2 writes each shared tile at the next free slot of its key (an LDS
+//    atomic), and each per-query tile at nshared + its rank among the
+//    per-query tiles in tile order, from per-chunk counts (no atomic, so no
+//    chain of atomic, shuffle and store per wave).
+template <int NT>
 __device__ void make_order(const OrderParams& p, OrderSmem& sm) {
+  static_assert(NT % 64 == 0 && NT / 64 <= kOrderThreads / 64, "wave counts fit wcount");
+  // with the keys cached: tiles per thread whose metadata loads are issued
+  // together (one round covers NT * kOrderLoad tiles)
+  constexpr int kOrderLoad = NT >= 1024 ? 8 : 16;
+  static_assert(kOrderKeyCache % (NT * kOrderLoad) == 0, "whole load rounds");
+  constexpr int kW = NT / 64;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const unsigned long long below = (1ull << lane) - 1ull;
   const int32_t* meta = p.meta;
   const int ntiles = p.ntiles;
-  for (int i = tid; i < kOrderKeysPadded; i += kThreads) sm.pos[i] = 0;
+  for (int i = tid; i < kOrderKeysPadded; i += NT) sm.pos[i] = 0;
   __syncthreads();
+  auto key_of = [](int nU, int mode) {
+    return mode == kModeShared ? (nU + kTileRows - 1) / kTileRows + 1 : 0;
+  };
   auto key = [&](int t) {
     const int32_t* mt = meta + int64_t(t) * kMetaInts;
-    return mt[1] == kModeShared ? (mt[0] + kTileRows - 1) / kTileRows + 1 : 0;
+    return key_of(mt[0], mt[1]);
   };
   const bool cached = ntiles <= kOrderKeyCache;
   auto keys = [&](int t0, int (&k)[kOrderPer], bool from_lds) {
 #pragma unroll
     for (int u = 0; u < kOrderPer; ++u) {
-      const int t = t0 + u * kThreads + tid;
+      const int t = t0 + u * NT + tid;
       k[u] = t >= ntiles ? -1 : from_lds ? int(sm.key[t]) : key(t);
     }
   };
-  // Key 0 (every per-query tile) is counted per wave: one LDS atomic per wave
-  // instead of one per tile on a single word.
-  for (int t0 = 0; t0 < ntiles; t0 += kThreads * kOrderPer) {
-    int k[kOrderPer];
-    keys(t0, k, false);
+  if (cached) {
+    for (int t0 = 0; t0 < ntiles; t0 += NT * kOrderLoad) {
+      int2 mv[kOrderLoad];
 #pragma unroll
-    for (int u = 0; u < kOrderPer; ++u) {
-      const unsigned long long z = __ballot(k[u] == 0);
-      if (k[u] > 0) atomicAdd(&sm.pos[k[u]], 1);
-      if (lane == 0 && z != 0ull) atomicAdd(&sm.pos[0], __popcll(z));
-      if (cached && k[u] >= 0) sm.key[t0 + u * kThreads + tid] = uint16_t(k[u]);
+      for (int u = 0; u < kOrderLoad; ++u) {  // clamped, so that every load is issued
+        const int t = min(t0 + u * NT + tid, ntiles - 1);
+        mv[u] = *reinterpret_cast<const int2*>(meta + int64_t(t) * kMetaInts);
+      }
+#pragma unroll
+      for (int u = 0; u < kOrderLoad; ++u) {
+        if (t0 + u * NT >= ntiles) break;  // (uniform) the rest of the round is past the end
+        const int t = t0 + u * NT + tid;
+        const int k = t >= ntiles ? -1 : key_of(mv[u].x, mv[u].y);
+        const unsigned long long z = __ballot(k == 0);
+        if (k > 0) atomicAdd(&sm.pos[k], 1);
+        if (lane == 0 && t - lane < ntiles) sm.zpre[(t - lane) / 64] = __popcll(z);
+        if (lane == 0 && z != 0ull) atomicAdd(&sm.pos[0], __popcll(z));
+        if (k >= 0) sm.key[t] = uint16_t(k);
+      }
+    }
+  } else {
+    // Key 0 (every per-query tile) is counted per wave: one LDS atomic per
+    // wave instead of one per tile on a single word.
+    for (int t0 = 0; t0 < ntiles; t0 += NT * kOrderPer) {
+      int k[kOrderPer];
+      keys(t0, k, false);
+#pragma unroll
+      for (int u = 0; u < kOrderPer; ++u) {
+        const unsigned long long z = __ballot(k[u] == 0);
+        if (k[u] > 0) atomicAdd(&sm.pos[k[u]], 1);
+        if (lane == 0 && z != 0ull) atomicAdd(&sm.pos[0], __popcll(z));
+      }
     }
   }
   __syncthreads();
   const int nshared = ntiles - sm.pos[0];  // shared tiles: every key above 0
   __syncthreads();  // every thread has read pos[0] before the scan rewrites it
-  static_assert(kOrderPlaceMax <= kThreads * kOrderPer && kOrderPlaceMax <= kOrderKeyCache,
+  static_assert(kOrderPlaceMax <= NT * kOrderPer && kOrderPlaceMax <= kOrderKeyCache &&
+                    kOrderPlaceMax % NT == 0,
                 "placement reads one pass of cached keys");
   if (nshared <= p.cus && ntiles <= kOrderPlaceMax) {
     // Every shared tile starts at once: XCD-local placement (see above). A
@@ -1332,16 +1400,16 @@ __device__ void make_order(const OrderParams& p, OrderSmem& sm) {
     // per-query tiles' entries fill the slots after them.
     int k[kOrderPer];
     keys(0, k, true);
-    int carry = 0;  // shared tiles of the earlier blocks of kThreads tiles
+    int carry = 0;  // shared tiles of the earlier blocks of NT tiles
 #pragma unroll
-    for (int u = 0; u < kOrderPlaceMax / kThreads; ++u) {
-      const int t = u * kThreads + tid;
+    for (int u = 0; u < kOrderPlaceMax / NT; ++u) {
+      const int t = u * NT + tid;
       const bool sh = k[u] > 0;
       const unsigned long long bm = __ballot(sh);
       if (lane == 0) sm.wcount[wave] = __popcll(bm);
       __syncthreads();
       int rank = carry + __popcll(bm & below);
-      for (int w = 0; w < kWaves; ++w) {
+      for (int w = 0; w < kW; ++w) {
         const int c = sm.wcount[w];
         rank += w < wave ? c : 0;
         carry += c;
@@ -1380,14 +1448,32 @@ __device__ void make_order(const OrderParams& p, OrderSmem& sm) {
       sm.pos[k] = carry + incl - v;
       carry += __shfl(incl, 63);
     }
+  } else if (wave == 1 && cached) {
+    wave_exclusive_scan(sm.zpre, (ntiles + 63) / 64);
   }
   __syncthreads();
-  for (int t0 = 0; t0 < ntiles; t0 += kThreads * kOrderPer) {
+  if (cached) {
+    for (int t0 = 0; t0 < ntiles; t0 += NT * kOrderPer) {
+#pragma unroll
+      for (int u = 0; u < kOrderPer; ++u) {
+        if (t0 + u * NT >= ntiles) break;  // (uniform)
+        const int t = t0 + u * NT + tid;
+        const int k = t >= ntiles ? -1 : int(sm.key[t]);
+        const unsigned long long z = __ballot(k == 0);
+        if (k > 0)
+          p.order[atomicAdd(&sm.pos[k], 1)] = (k << kOrderTileBits) | t;
+        else if (k == 0)
+          p.order[nshared + sm.zpre[(t - lane) / 64] + __popcll(z & below)] = t;
+      }
+    }
+    return;
+  }
+  for (int t0 = 0; t0 < ntiles; t0 += NT * kOrderPer) {
     int k[kOrderPer];
-    keys(t0, k, cached);
+    keys(t0, k, false);
 #pragma unroll
     for (int u = 0; u < kOrderPer; ++u) {
-      const int t = t0 + u * kThreads + tid;
+      const int t = t0 + u * NT + tid;
       const unsigned long long z = __ballot(k[u] == 0);
       int base = 0;
       if (lane == 0 && z != 0ull) base = atomicAdd(&sm.pos[0], __popcll(z));
@@ -1431,7 +1517,7 @@ __global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
     int64_t t = blockIdx.x;
     if (p.ord.order != nullptr) {
       if (t == 0) {
-        make_order(p.ord, sm.o);
+        make_order<kThreads>(p.ord, sm.o);
         return;
       }
       --t;
@@ -1451,6 +1537,17 @@ __global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
       __syncthreads();  // every wave is done with the LDS before the next query
     }
   }
+}
+
+// The tile order as a launch of its own: one work-group of kOrderThreads
+// threads, where the per-query launch would only make the order (the short
+// queries of a tile plan run in sa_fwd_wave_kernel, and an index plan). A
+// quarter of the work per wave against the per-query launch's work-group 0:
+// at 8 192 tiles the order took 14.3 us there (21.8 before its metadata
+// loads were issued together and its per-query slots were counted per chunk).
+__global__ void __launch_bounds__(kOrderThreads) sa_order_kernel(const OrderParams p) {
+  __shared__ __attribute__((aligned(16))) OrderSmem sm;
+  make_order<kOrderThreads>(p, sm);
 }
 
 // ============================================================================
@@ -2794,7 +2891,8 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
     }
     // The per-query launch: one work-group per tile runs the queries of a
     // per-query tile (the others return at once), and work-group 0 makes the
-    // tile order when this call makes one (only that, for an index plan).
+    // tile order when this call makes one (an index plan and a short-query
+    // plan make it in sa_order_kernel instead, below).
     // (Running a placed call's per-query tiles in the tile kernel instead,
     // through the branch that reruns aborted tiles, makes the compiler spill
     // the kernel's 256 AGPR accumulators.)
@@ -2806,14 +2904,15 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
       p.ord.ntiles = int(plan.ntiles);
       p.ord.cus = cus;
     }
-    // Short queries run per query as one wave each (sa_fwd_wave_kernel); the
-    // tile order, when this call makes one, is then made by a one-work-group
-    // per-query launch before it.
+    // An index plan makes only the union and the order; short queries run
+    // per query as one wave each (sa_fwd_wave_kernel). In both the tile
+    // order, when the call makes one, has a launch of its own.
+    if (what == Launch::kPlanOnly)
+      return run(SA_KERNEL_ORDER, fn(sa_order_kernel), dim3(1), dim3(kOrderThreads), 0, &p.ord);
     if (wave_ok) {
       if (p.ord.order != nullptr) {
-        p.nblocks = 1;
-        const int orc = run(SA_KERNEL_QUERY, fn(sa_fwd_query_kernel<2, true>), dim3(1),
-                            dim3(kThreads), 0, &p);
+        const int orc =
+            run(SA_KERNEL_ORDER, fn(sa_order_kernel), dim3(1), dim3(kOrderThreads), 0, &p.ord);
         if (orc != SA_OK) return orc;
         p.ord.order = nullptr;
       }
@@ -2821,9 +2920,9 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
                           dim3(unsigned(plan.ntiles * (kTQ / kWQueries))), dim3(64), 0, &p);
       if (wrc != SA_OK) return wrc;
     } else {
-      p.nblocks = what == Launch::kPlanOnly ? 1 : plan.ntiles + (p.ord.order != nullptr ? 1 : 0);
+      p.nblocks = plan.ntiles + (p.ord.order != nullptr ? 1 : 0);
       const int lrc = launch_query();
-      if (lrc != SA_OK || what == Launch::kPlanOnly) return lrc;
+      if (lrc != SA_OK) return lrc;
     }
 
     TileParams tp{};

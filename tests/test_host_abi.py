@@ -162,7 +162,7 @@ def test_library_exports_every_declared_symbol(libs):
     hip, _ = libs
     for name in declared_functions():
         assert hasattr(hip, name), f"{name} not exported"
-    assert hip.sa_abi_version() == 7
+    assert hip.sa_abi_version() == 8
     # the allocation-free entry point and its device array live in their own
     # library, so sa_forward's callers do not carry the array
     assert not hasattr(hip, "sa_forward_noalloc")
