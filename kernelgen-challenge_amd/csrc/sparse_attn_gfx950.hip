@@ -375,16 +375,28 @@ __device__ __forceinline__ void dma_barrier() {
   asm volatile("" ::: "memory");
 }
 
-__device__ __forceinline__ float wave_max16(float x) {  // over lanes n, n+16, n+32, n+48
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
+// Reductions over lanes n, n + 16, n + 32, n + 48 (the four lane rows of a
+// wave64). v_permlane16_swap with both operands x gives lane n the values of
+// lanes n and n ^ 16 (as its two results), v_permlane32_swap those of n and
+// n ^ 32: two VALU instructions per level, against __shfl_xor's
+// ds_bpermute (an LDS round trip plus its index arithmetic). The sums add in
+// the same order as a butterfly: (x[n] + x[n^16]) + (x[n^32] + x[n^48]).
+__device__ __forceinline__ float wave_max16(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 
 __device__ __forceinline__ float wave_sum16(float x) {
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // ============================================================================
@@ -537,14 +549,16 @@ __device__ __forceinline__ void query_step(const FwdParams& p, QuerySmemT<kRing>
   const float mstep = fmaxf(fmaxf(s_red[0][n], s_red[1][n]), fmaxf(s_red[2][n], s_red[3][n]));
   float alpha = 1.f;
   if (mstep > m_run + kRescaleLog2) {
-    alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mstep);  // O, l still 0 at first
+    // v_exp_f32 as is: exp2f adds a rescale for results below 2^-126, which
+    // are negligible next to the running sum (at least 1)
+    alpha = m_run == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - mstep);
     m_run = mstep;
   }
   float psum = 0.f;
   bf16x4 pb;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const float pj = exp2f(sv[j] - m_run);
+    const float pj = __builtin_amdgcn_exp2f(sv[j] - m_run);
     psum += pj;
     pb[j] = static_cast<__bf16>(pj);
   }
@@ -1840,14 +1854,15 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
       mx = wave_max16(mx);  // finite: the step's row 0 is valid
       float alpha = 1.f;
       if (mx > m_run + kRescaleLog2) {
-        alpha = m_run == -INFINITY ? 1.f : exp2f(m_run - mx);  // O, l still 0 at first
+        // (O, l still 0 at first; v_exp_f32 as in the per-query step)
+        alpha = m_run == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - mx);
         m_run = mx;
       }
       float psum = 0.f;
       bf16x4 pb;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const float pk = exp2f(sv[k] - m_run);
+        const float pk = __builtin_amdgcn_exp2f(sv[k] - m_run);
         psum += pk;
         pb[k] = static_cast<__bf16>(pk);
       }
