@@ -1588,6 +1588,7 @@ __global__ void __launch_bounds__(kOrderThreads) sa_order_kernel(const OrderPara
 constexpr int kWRows = 16;               // rows per step
 constexpr int kWPitch = kRowBytes + 48;  // LDS row pitch (bytes)
 constexpr int kWQueries = 2;             // queries per work-group
+constexpr int kWVAhead = 8;              // V fragments in flight in O += P . V
 // Slots per query the list holds. Against the 4-wave per-query kernel: topk
 // 128 1365 -> 1102 us/call at 64 x 1024 queries, topk 640 1232 -> 1260 at
 // 1 x 16384 (a longer list amortises that kernel's start), so the cap sits
@@ -1840,6 +1841,13 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
         s_chain(std::true_type{});
       else
         s_chain(std::false_type{});
+      // The first V fragments of O += P . V (they do not depend on P) are
+      // read now, so that their LDS latency passes under the softmax: lane
+      // (n, g) reads V[rows 4g .. 4g + 3][16 blk + n] of column block blk.
+      const uint8_t* vb = tb + (4 * g + (n >> 2)) * kWPitch + 8 * (n & 3);
+      bf16x4 vf[kWVAhead];
+#pragma unroll
+      for (int i = 0; i < kWVAhead; ++i) vf[i] = lds_read_tr16(vb + 32 * i);
       mfma_agpr_drain();  // S^T is read by VALU below
       if (s == ns - 1 && jn < nq) load_q(jn);  // Q^T is no longer read
 
@@ -1877,16 +1885,15 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
           for (int k = 0; k < 4; ++k) oacc[blk][k] *= ak[k];
       }
 
-      // O += P . V: lane (n, g) reads V[rows 4g .. 4g + 3][16 blk + n]; the V
-      // fragments of 16 column blocks read ahead of their MFMAs
-      const uint8_t* vb = tb + (4 * g + (n >> 2)) * kWPitch + 8 * (n & 3);
+      // O += P . V over the 32 column blocks, each V fragment read kWVAhead
+      // MFMAs ahead of its own (the MFMA takes 16 cycles, an LDS read about
+      // 100: left to itself the compiler read 3 ahead and each MFMA waited)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        bf16x4 vf[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) vf[i] = lds_read_tr16(vb + 32 * (16 * h + i));
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[16 * h + i] = mfma_16x16x16(pb, vf[i], oacc[16 * h + i]);
+      for (int i = 0; i < 32; ++i) {
+        const bf16x4 v = vf[i % kWVAhead];
+        if (i + kWVAhead < 32) vf[i % kWVAhead] = lds_read_tr16(vb + 32 * (i + kWVAhead));
+        oacc[i] = mfma_16x16x16(pb, v, oacc[i]);
+        __builtin_amdgcn_sched_barrier(0);  // keep the interleave
       }
     }
     if (ns > 0 && jn < nq) qloaded = jn;
