@@ -1034,10 +1034,15 @@ __device__ __forceinline__ void query_stream(const FwdParams& p, int64_t bi, int
 //     ascending row order with consecutive lanes on consecutive entries.
 // 1024 threads with 2 vectors per round from kIdxWideKv rows (the count
 // table then allows one work-group per CU): the 1x16384 kv_len 16384 topk 128
-// shape's index kernel 31.6 -> 26.1 us; 512 threads with 4 vectors below.
+// shape's index kernel 31.6 -> 26.1 us; 512 threads with 4 vectors below,
+// and 256 threads for tiles of at most 4 096 slots (one round of 1 or 4
+// vectors per thread, and twice the work-groups per CU): the contest shapes'
+// index kernel 64x1024-1024-128 36.7 -> 13.2 us, 16x4096-4096-128 40.0 ->
+// 21.3, 64x1024-1280-384 101 -> 73 (A/B, same box).
 constexpr int kIdxThreadsNarrow = 512;
 constexpr int kIdxVecNarrow = 4;    // index vectors per thread per round
 constexpr int64_t kIdxWideKv = 8192;
+constexpr int kIdxSmallSlots = 4096;  // tile slots (8 topk) up to which 256 threads
 constexpr int kIdxScan = 4;   // LDS chunk reads per wave per batch
 
 template <int kIdxThreads, int kIdxVec>
@@ -2902,13 +2907,21 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
       // long caches (one work-group per CU by LDS): twice the threads, half
       // the index vectors each
       const bool wide = a->kv_len >= kIdxWideKv;
-      const void* ik = wide ? reinterpret_cast<const void*>(sa_tile_index_kernel<1024, 2>)
-                            : reinterpret_cast<const void*>(sa_tile_index_kernel<kIdxThreadsNarrow, kIdxVecNarrow>);
+      // small tiles: 256 threads, one round of 1 or 4 index vectors each
+      const int64_t slots = kTQ * a->topk;
+      const bool small1 = !wide && slots <= 256 * 4;
+      const bool small4 = !wide && !small1 && slots <= kIdxSmallSlots;
+      const void* ik =
+          wide     ? reinterpret_cast<const void*>(sa_tile_index_kernel<1024, 2>)
+          : small1 ? reinterpret_cast<const void*>(sa_tile_index_kernel<256, 1>)
+          : small4 ? reinterpret_cast<const void*>(sa_tile_index_kernel<256, 4>)
+                   : reinterpret_cast<const void*>(sa_tile_index_kernel<kIdxThreadsNarrow, kIdxVecNarrow>);
       if (lds > 65536 &&
           hipFuncSetAttribute(ik, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
         return SA_EHIP;
       const int irc = run(SA_KERNEL_INDEX, ik, dim3(unsigned(plan.ntiles)),
-                          dim3(wide ? 1024 : kIdxThreadsNarrow), uint32_t(lds), &ip);
+                          dim3(wide ? 1024 : (small1 || small4) ? 256 : kIdxThreadsNarrow),
+                          uint32_t(lds), &ip);
       if (irc != SA_OK) return irc;
     }
     // The per-query launch: one work-group per tile runs the queries of a
