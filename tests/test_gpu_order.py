@@ -103,6 +103,9 @@ def test_tile_order(name):
     assert torch.equal(keys, want_key[tiles.long()])
     ns = int(shared.sum())
     assert bool((keys[:ns] > 0).all()) and bool((keys[ns:] == 0).all())
+    # up to the 16 384 tiles whose keys the order keeps in LDS, the per-query
+    # tiles are placed by rank (no atomics): in tile order
+    assert bool((tiles[ns:][1:] > tiles[ns:][:-1]).all()), "per-query tiles in tile order"
     if ns > cus:
         assert bool((keys[:ns][1:] <= keys[:ns][:-1]).all()), "longest first"
     else:
@@ -111,3 +114,48 @@ def test_tile_order(name):
         first = [sum(counts[:x]) for x in range(XCDS)]
         want = [ids[first[s % XCDS] + s // XCDS] for s in range(ns)]
         assert tiles[:ns].tolist() == want
+
+
+def test_tile_order_beyond_key_cache():
+    """More tiles (16 400) than the order keeps keys for in LDS (16 384): the
+    keys are loaded again in the second pass and per-query tiles are placed
+    by one LDS atomic per wave. Tiles alternate in runs between 32 shared
+    rows (every query of the tile names the same window: shared) and 32
+    random rows of 4 096 per query (union about 250 rows: per query). Only
+    the plan runs (sa_plan_indices); q and o are allocated, never read."""
+    b, m, kv_len, topk = 1, 8 * 16400, 4096, 32
+    say(f"tile order beyond the key cache: {m // 8} tiles")
+    g = torch.Generator().manual_seed(21)
+    t = torch.arange(m)
+    win = ((torch.arange(topk)[None] + 64 * ((t // 8) % 60)[:, None]) % kv_len).to(torch.int32)
+    rnd = torch.randint(0, kv_len, (m, topk), generator=g, dtype=torch.int32)
+    sel = (((t // 8) // 7) % 2 == 0)[:, None]
+    idx = torch.where(sel, win, rnd)[None].to(DEV)
+    q = torch.empty(b, m, 16, 512, dtype=torch.bfloat16, device=DEV)
+    kv = torch.randn(b, kv_len, 512, generator=g).to(torch.bfloat16).to(DEV)
+    sink = torch.zeros(16, device=DEV)
+    o = torch.empty_like(q)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    lib = sa_capi.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    a = sa_capi.make_args(q, kv, sink, idx, o, wl.SCALE)
+    p = host_plan(a, cus)
+    assert p["tiles"] == 1 and p["ntiles"] == 16400
+    n = sa_capi.workspace_bytes(lib, a)
+    ws = torch.full((n,), 0xAB, dtype=torch.uint8, device=DEV)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), n
+    sa_capi.check(lib, lib.sa_plan_indices(ctypes.byref(a), ctypes.c_void_p(stream)), "plan")
+    torch.cuda.synchronize()
+    nt = p["ntiles"]
+    meta = ws[p["meta_off"]:p["meta_off"] + 16 * nt].view(torch.int32).view(nt, 4).cpu()
+    order = ws[p["order_off"]:p["order_off"] + 4 * nt].view(torch.int32).cpu()
+    shared = meta[:, 1] == MODE_SHARED
+    ns = int(shared.sum())
+    assert 0 < ns < nt, "the case needs shared and per-query tiles"
+    want_key = torch.where(shared, (meta[:, 0] + 63) // 64 + 1, torch.zeros_like(meta[:, 0]))
+    tiles = order & ((1 << TILE_BITS) - 1)
+    keys = order >> TILE_BITS
+    assert torch.equal(torch.sort(tiles).values, torch.arange(nt, dtype=torch.int32))
+    assert torch.equal(keys, want_key[tiles.long()])
+    assert bool((keys[:ns] > 0).all()) and bool((keys[ns:] == 0).all())
+    assert bool((keys[:ns][1:] <= keys[:ns][:-1]).all()), "longest first"
