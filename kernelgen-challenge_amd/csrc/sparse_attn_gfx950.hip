@@ -2199,6 +2199,17 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       sacc0[i] = 0.f;
       sacc1[i] = 0.f;
     }
+    // Pair skipping also skips S^T: wave w computes S^T for pair w only, so
+    // a half of the step that the pair does not name takes none of its 32
+    // MFMAs (its scores would all be -inf: p = 0, the sums and the reference
+    // unchanged, and P.V skips the block). Both halves named: the dense
+    // chain.
+    bool sthalf0 = true, sthalf1 = true;
+    if constexpr (kSkip) {
+      pair_activity();
+      sthalf0 = ((act0 >> wave) & 1u) != 0u;
+      sthalf1 = ((act1 >> wave) & 1u) != 0u;
+    }
     {
       const uint8_t* kr = tb + koff;
       bf16x8 kf[kKRing];
@@ -2206,23 +2217,47 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
         kf[slot] =
             *reinterpret_cast<const bf16x8*>(kr + (i >> 5) * 32 * kTilePitch + 32 * (i & 31));
       };
-#pragma unroll
-      for (int i = 0; i < kKRing - 1; ++i) kread(i, i);
       float mx = -INFINITY, mref = 0.f, psum = 0.f;
       bf16x4 pk;
+      // S^T over the MFMAs [kLo, kHi) of the 64 (32 per half). The gathers ride
+      // the first half's MFMAs (when the chain starts at 0); the softmax of rows
+      // 0..31 rides the second half's when the chain is whole.
+      auto st_chain = [&](auto lo_c, auto hi_c) {
+        constexpr int kLo = decltype(lo_c)::value, kHi = decltype(hi_c)::value;
 #pragma unroll
-      for (int i = 0; i < 2 * (kDim / 16); ++i) {
-        if (i + kKRing - 1 < 2 * (kDim / 16)) kread(i + kKRing - 1, (i + kKRing - 1) % kKRing);
-        if (i < kDim / 16)
-          sacc0 = mfma_32x32x16(kf[i % kKRing], qf[i], sacc0);
-        else
-          sacc1 = mfma_32x32x16(kf[i % kKRing], qf[i - kDim / 16], sacc1);
-        if (i % kDmaEvery == kDmaEvery - 1 && i / kDmaEvery < kRowsPerWave)
-          dma_row(rows_next, i / kDmaEvery, buf ^ 1);
-        if (i == 1) dma_counts(nxt, buf ^ 1);
-        if (i >= kDim / 16) sm_slot(i - kDim / 16, sacc0, lc0, 0, mx, mref, psum, pk);
+        for (int i = kLo; i < kLo + kKRing - 1; ++i) kread(i, i % kKRing);
+#pragma unroll
+        for (int i = kLo; i < kHi; ++i) {
+          if (i + kKRing - 1 < kHi) kread(i + kKRing - 1, (i + kKRing - 1) % kKRing);
+          if (i < kDim / 16)
+            sacc0 = mfma_32x32x16(kf[i % kKRing], qf[i], sacc0);
+          else
+            sacc1 = mfma_32x32x16(kf[i % kKRing], qf[i - kDim / 16], sacc1);
+          if (kLo == 0 && i % kDmaEvery == kDmaEvery - 1 && i / kDmaEvery < kRowsPerWave)
+            dma_row(rows_next, i / kDmaEvery, buf ^ 1);
+          if (kLo == 0 && i == 1) dma_counts(nxt, buf ^ 1);
+          if (kLo == 0 && kHi == 2 * (kDim / 16) && i >= kDim / 16)
+            sm_slot(i - kDim / 16, sacc0, lc0, 0, mx, mref, psum, pk);
 
-        __builtin_amdgcn_sched_barrier(0);  // keep the interleave
+          __builtin_amdgcn_sched_barrier(0);  // keep the interleave
+        }
+      };
+      using I0 = std::integral_constant<int, 0>;
+      using I32 = std::integral_constant<int, kDim / 16>;
+      using I64 = std::integral_constant<int, 2 * (kDim / 16)>;
+      if (!kSkip || (sthalf0 && sthalf1)) {
+        st_chain(I0{}, I64{});
+      } else {
+        if (sthalf0) {
+          st_chain(I0{}, I32{});
+#pragma unroll
+          for (int j = 0; j < kSmSlots; ++j) sm_slot(j, sacc0, lc0, 0, mx, mref, psum, pk);
+        } else {
+#pragma unroll
+          for (int i = 0; i < kRowsPerWave; ++i) dma_row(rows_next, i, buf ^ 1);
+          dma_counts(nxt, buf ^ 1);
+        }
+        if (sthalf1) st_chain(I32{}, I64{});
       }
       l_run += psum;
     }
@@ -2300,14 +2335,13 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
       // interleaving such branches would sit around the softmax, and the
       // compiler then spills its state). Per accumulator the MFMAs run in the
       // dense form's order, so the sums are the same.
-      {
+      if (sthalf1) {  // (a half the pair does not name has no P to read)
         float mx = -INFINITY, mref = 0.f, psum = 0.f;
         bf16x4 pk;
 #pragma unroll
         for (int j = 0; j < kSmSlots; ++j) sm_slot(j, sacc1, lc1, 1, mx, mref, psum, pk);
         l_run += psum;
       }
-      pair_activity();
       auto pread = [&](bf16x8 (&af)[2][4], int kb0) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
