@@ -1562,8 +1562,9 @@ __global__ void __launch_bounds__(kThreads, kRing == 2 ? 2 : 1)
 // threads, where the per-query launch would only make the order (the short
 // queries of a tile plan run in sa_fwd_wave_kernel, and an index plan). A
 // quarter of the work per wave against the per-query launch's work-group 0:
-// at 8 192 tiles the order took 14.3 us there (21.8 before its metadata
-// loads were issued together and its per-query slots were counted per chunk).
+// at 8 192 tiles the order takes 7.2 us here, 14.3 there (21.8 before its
+// metadata loads were issued together and its per-query slots were counted
+// per chunk).
 __global__ void __launch_bounds__(kOrderThreads) sa_order_kernel(const OrderParams p) {
   __shared__ __attribute__((aligned(16))) OrderSmem sm;
   make_order<kOrderThreads>(p, sm);
