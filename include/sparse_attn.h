@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 8
+#define SA_ABI_VERSION 9
 
 /* Return codes. */
 enum {
@@ -73,7 +73,13 @@ enum {
      row of a 32-row half-step and skip its P . V), the dense form otherwise.
      These force one form; both give the same results. Not both at once. */
   SA_FLAG_TILE_SKIP = 8u,
-  SA_FLAG_TILE_DENSE = 16u
+  SA_FLAG_TILE_DENSE = 16u,
+  /* (ABI version 9) tile plans with topk <= 384 (per-query queries run as
+     WAVE): run the shared-row tiles from the tile order, one work-group per
+     tile, after an ORDER launch (none with SA_FLAG_PLANNED), instead of the
+     default TILE launch of one work-group per CU that walks the tiles' modes
+     and runs the shared ones. Same results. */
+  SA_FLAG_TILE_ORDERED = 32u
 };
 
 /*
@@ -209,11 +215,14 @@ int sa_plan_indices(const sa_args* a, void* hip_stream);
  * its own.) Version 6: unsplit plans with topk <= 384 run their per-query
  * queries as WAVE instead, one wave per query. Version 8: where QUERY would
  * only make the tile order (such a plan, and sa_plan_indices), the order is
- * ORDER, a one-work-group launch of its own: INDEX, ORDER, WAVE, TILE.
+ * ORDER, a one-work-group launch of its own. Version 9: such a plan makes no
+ * order (INDEX, WAVE, TILE; its TILE launch finds the shared tiles itself)
+ * unless SA_FLAG_TILE_ORDERED asks for INDEX, ORDER, WAVE, TILE;
+ * sa_plan_indices still makes it (INDEX, ORDER).
  */
 enum {
   SA_KERNEL_INDEX = 0,    /* row unions of shared-row tiles (tile plans)   */
-  SA_KERNEL_ORDER = 1,    /* the tile order alone (version 8; see above)   */
+  SA_KERNEL_ORDER = 1,    /* the tile order alone (versions 8, 9; above)   */
   SA_KERNEL_TILE = 2,     /* shared-row tiles (tile plans)                 */
   SA_KERNEL_QUERY = 3,    /* per-query parts; in tile plans the per-query
                              tiles and the tile order                      */

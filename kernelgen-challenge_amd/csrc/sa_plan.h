@@ -99,7 +99,7 @@ inline int validate(const sa_args* a) {
     return SA_EINVAL;
   if (!heads_supported(a->h) || a->d != kDim) return SA_EUNSUPPORTED;
   if ((a->flags & ~uint32_t(SA_FLAG_PER_QUERY | SA_FLAG_FORCE_TILES | SA_FLAG_PLANNED |
-                            SA_FLAG_TILE_SKIP | SA_FLAG_TILE_DENSE)) != 0)
+                            SA_FLAG_TILE_SKIP | SA_FLAG_TILE_DENSE | SA_FLAG_TILE_ORDERED)) != 0)
     return SA_EINVAL;
   if ((a->flags & SA_FLAG_TILE_SKIP) != 0 && (a->flags & SA_FLAG_TILE_DENSE) != 0)
     return SA_EINVAL;

@@ -1962,42 +1962,30 @@ union TileQuerySmem {
   QuerySmem q;
 };
 
+// The order entry of a shared tile t with nU union rows: its step count plus
+// one above the tile (an all-masked tile has no step).
+__device__ __forceinline__ int32_t shared_entry(int64_t t, int nU) {
+  return int32_t(((1 + (nU + kTileRows - 1) / kTileRows) << kOrderTileBits) | int32_t(t));
+}
+
+// One shared tile, whose order entry is `entry` (a nonzero step key). It
+// returns with every transfer it issued complete.
 // kSkip: the pair-skipping form of the step (below, "Pair skipping"), for
 // tiles whose query pairs often name no row of a 32-row half-step; the dense
 // form otherwise. Their results are the same bits.
 template <bool kSkip>
-__global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
+__device__ __forceinline__ void tile_run(const TileParams p, const int32_t entry, const int tid) {
   __shared__ __attribute__((aligned(16))) TileQuerySmem sm;
   auto& s_tile = sm.t.tile;
   auto& s_p = sm.t.p;
   auto& s_lc = sm.t.lc;
   auto& s_abort = sm.t.abort;
 
-  const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
-  int32_t entry;
-  if (p.placed) {
-    // At most one tile per CU and at least one per two, all starting at once:
-    // the order kernel's XCD-local placement, computed here (work-group i runs
-    // on XCD i % 8; XCD x takes the x-th eighth of the tiles in tile order).
-    const int n = int(p.ntiles);
-    const int x = int(blockIdx.x) % kXcds;
-    int first = 0;
-    for (int y = 0; y < x; ++y) first += (n - y + kXcds - 1) / kXcds;
-    const int t = first + int(blockIdx.x) / kXcds;
-    const int32_t* mt = p.meta + int64_t(t) * kMetaInts;
-    const int nU = __builtin_amdgcn_readfirstlane(mt[0]);
-    const bool shared = __builtin_amdgcn_readfirstlane(mt[1]) == kModeShared;
-    entry = shared ? int32_t(((1 + (nU + kTileRows - 1) / kTileRows) << kOrderTileBits) | t) : 0;
-  } else {
-    entry = p.order[blockIdx.x];  // one load: tile and step count
-  }
-  // a per-query tile: its queries run in the per-query launch
-  if ((entry >> kOrderTileBits) == 0) return;
   const int64_t tile = entry & ((1 << kOrderTileBits) - 1);
   const int nsteps = (entry >> kOrderTileBits) - 1;
   const int64_t bi = tile / p.tiles_per_b;
@@ -2447,6 +2435,62 @@ __global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TilePara
         }
       }
     }
+}
+
+// kScan = false: work-group i runs entry order[i] (one work-group per tile;
+// those of per-query tiles return at once), or the placed launch's tile i.
+// kScan = true (short-query plans, whose per-query tiles run in
+// sa_fwd_wave_kernel, so that most tiles are usually per-query): a grid of G
+// work-groups, one per CU, where work-group b walks the tiles b, b + G,
+// b + 2G, ... and runs the shared ones; no order is made. One work-group per
+// tile at one per CU (by LDS) made a launch whose 8 192 tiles were all
+// per-query take 14.8 us, its work-groups each only reading the order entry.
+template <bool kSkip, bool kScan>
+__global__ void __launch_bounds__(kThreads, 1) sa_fwd_tile_kernel(const TileParams p) {
+  if constexpr (kScan) {
+    const int64_t G = gridDim.x;
+    const int lane = threadIdx.x & 63;
+    for (int64_t t0 = blockIdx.x; t0 < p.ntiles; t0 += 64 * G) {
+      // lane i tests tile t0 + iG; every wave reads the same modes, so the
+      // mask, and with it the loop below, is the same in all four
+      const int64_t tl = t0 + lane * G;
+      const bool sh = tl < p.ntiles && p.meta[tl * kMetaInts + 1] == kModeShared;
+      uint64_t mask = __ballot(sh);
+      while (mask != 0) {
+        const int64_t t = t0 + int64_t(__builtin_ctzll(mask)) * G;
+        mask &= mask - 1;
+        const int nU = __builtin_amdgcn_readfirstlane(p.meta[t * kMetaInts]);
+        const __attribute__((address_space(4))) TileParams* pk =
+            (const __attribute__((address_space(4))) TileParams*)__builtin_amdgcn_kernarg_segment_ptr();
+        int tid = threadIdx.x;
+        asm volatile("" : "+s"(pk), "+v"(tid));
+        tile_run<kSkip>(*(const TileParams*)(const void*)pk, shared_entry(t, nU), tid);
+        __syncthreads();  // the next tile's gathers overwrite this one's LDS
+      }
+    }
+  } else {
+    int32_t entry;
+    if (p.placed) {
+      // At most one tile per CU and at least one per two, all starting at
+      // once: the order kernel's XCD-local placement, computed here
+      // (work-group i runs on XCD i % 8; XCD x takes the x-th eighth of the
+      // tiles in tile order).
+      const int n = int(p.ntiles);
+      const int x = int(blockIdx.x) % kXcds;
+      int first = 0;
+      for (int y = 0; y < x; ++y) first += (n - y + kXcds - 1) / kXcds;
+      const int t = first + int(blockIdx.x) / kXcds;
+      const int32_t* mt = p.meta + int64_t(t) * kMetaInts;
+      const int nU = __builtin_amdgcn_readfirstlane(mt[0]);
+      const bool shared = __builtin_amdgcn_readfirstlane(mt[1]) == kModeShared;
+      entry = shared ? shared_entry(t, nU) : 0;
+    } else {
+      entry = p.order[blockIdx.x];  // one load: tile and step count
+    }
+    // a per-query tile: its queries run in the per-query launch
+    if ((entry >> kOrderTileBits) == 0) return;
+    tile_run<kSkip>(p, entry, threadIdx.x);
+  }
 }
 
 // ============================================================================
@@ -2974,13 +3018,16 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
       p.ord.ntiles = int(plan.ntiles);
       p.ord.cus = cus;
     }
-    // An index plan makes only the union and the order; short queries run
-    // per query as one wave each (sa_fwd_wave_kernel). In both the tile
-    // order, when the call makes one, has a launch of its own.
+    // An index plan makes only the union and the order, the latter in a
+    // launch of its own. Short queries run per query as one wave each
+    // (sa_fwd_wave_kernel), and their call makes no order: its tile launch
+    // walks the tiles' modes itself (the scan form below), unless a flag
+    // asks for the ordered launch.
     if (what == Launch::kPlanOnly)
       return run(SA_KERNEL_ORDER, fn(sa_order_kernel), dim3(1), dim3(kOrderThreads), 0, &p.ord);
+    const bool scan = wave_ok && (a->flags & SA_FLAG_TILE_ORDERED) == 0;
     if (wave_ok) {
-      if (p.ord.order != nullptr) {
+      if (!scan && p.ord.order != nullptr) {
         const int orc =
             run(SA_KERNEL_ORDER, fn(sa_order_kernel), dim3(1), dim3(kOrderThreads), 0, &p.ord);
         if (orc != SA_OK) return orc;
@@ -3023,13 +3070,19 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
     tp.fwd = p;
     tp.placed = placed ? 1 : 0;
     tp.meta = ip.meta;
-    // One work-group per tile; those of per-query tiles return at once.
+    // One work-group per tile (those of per-query tiles return at once), or
+    // after the wave launch one per CU that runs the shared tiles it finds.
     // The pair-skipping form when a row is named by fewer than one query of a
     // tile on average (high locality: 8 * 512 against 16 384 rows), unless a
     // flag forces one form.
     const bool skip = (a->flags & SA_FLAG_TILE_SKIP) != 0 ||
                       ((a->flags & SA_FLAG_TILE_DENSE) == 0 && kTQ * a->topk < a->kv_len);
-    return run(SA_KERNEL_TILE, skip ? fn(sa_fwd_tile_kernel<true>) : fn(sa_fwd_tile_kernel<false>),
+    if (scan)
+      return run(SA_KERNEL_TILE,
+                 skip ? fn(sa_fwd_tile_kernel<true, true>) : fn(sa_fwd_tile_kernel<false, true>),
+                 dim3(unsigned(std::min<int64_t>(plan.ntiles, cus))), dim3(kThreads), 0, &tp);
+    return run(SA_KERNEL_TILE,
+               skip ? fn(sa_fwd_tile_kernel<true, false>) : fn(sa_fwd_tile_kernel<false, false>),
                dim3(unsigned(plan.ntiles)), dim3(kThreads), 0, &tp);
   }
   if (what == Launch::kPlanOnly) return SA_OK;  // per-query plans keep no index state

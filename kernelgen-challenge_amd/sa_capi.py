@@ -21,7 +21,7 @@ NOALLOC_LIB_PATH = os.path.join(_HERE, "lib", "libsa_noalloc_gfx950.so")
 SA_OK, SA_EINVAL, SA_EUNSUPPORTED, SA_EWORKSPACE, SA_EHIP, SA_ESCRATCH = range(6)
 SA_NOALLOC_SCRATCH_BYTES = 48 << 20
 SA_FLAG_PER_QUERY, SA_FLAG_FORCE_TILES, SA_FLAG_PLANNED = 1, 2, 4
-SA_FLAG_TILE_SKIP, SA_FLAG_TILE_DENSE = 8, 16
+SA_FLAG_TILE_SKIP, SA_FLAG_TILE_DENSE, SA_FLAG_TILE_ORDERED = 8, 16, 32
 KERNELS = ("index", "order", "tile", "query", "combine", "wave")  # SA_KERNEL_* order
 SA_KERNEL_COUNT = len(KERNELS)
 

@@ -41,7 +41,7 @@ __all__ = ["sparse_attn", "sparse_attn_with_lse", "sparse_attn_merge", "sparse_a
            "IndexPlan", "set_index_check", "index_check_enabled", "index_check_mode",
            "check_index_errors", "set_path_flags",
            "load_extension", "extension_path", "FLAG_PER_QUERY", "FLAG_FORCE_TILES",
-           "FLAG_TILE_SKIP", "FLAG_TILE_DENSE",
+           "FLAG_TILE_SKIP", "FLAG_TILE_DENSE", "FLAG_TILE_ORDERED",
            "hc_split_sinkhorn", "fused_moe"]
 
 _PKG_DIR = os.path.dirname(os.path.abspath(__file__))
@@ -71,6 +71,7 @@ FLAG_PER_QUERY = 1     # every query gathers its own rows
 FLAG_FORCE_TILES = 2   # every eligible 8-query tile shares its row union
 FLAG_TILE_SKIP = 8     # shared tiles use the pair-skipping step (same results)
 FLAG_TILE_DENSE = 16   # shared tiles use the dense step (same results)
+FLAG_TILE_ORDERED = 32  # short-query tile plans: ordered tile launch (same results)
 
 
 def extension_path() -> str:

@@ -24,7 +24,7 @@ def case(b, m, kv_len, topk, seed):
 
 
 @pytest.mark.parametrize("shape,expect", [
-    ((1, 64, 300, 64), INDEX | ORDER | WAVE | TILE),    # shared-row plan, short queries
+    ((1, 64, 300, 64), INDEX | WAVE | TILE),            # shared-row plan, short queries
     ((1, 300, 2048, 700), INDEX | QUERY | TILE),        # topk above the wave kernel's
     ((4, 1, 2048, 512), QUERY | COMBINE),               # split-topk plan
     ((1, 3, 2048, 64), WAVE),                           # per query, no split

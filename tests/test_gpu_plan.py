@@ -119,9 +119,9 @@ def test_plan_of_an_aborting_tile(gpu_sa):
 
 
 @pytest.mark.parametrize("shape,plain,planned", [
-    # short queries: one wave each; the plain call's ORDER launch makes the
-    # tile order, which a planned call already has
-    ((1, 64, 300, 64), INDEX | ORDER | WAVE | TILE, WAVE | TILE),
+    # short queries: one wave each; neither call launches ORDER (the tile
+    # launch walks the tiles' modes)
+    ((1, 64, 300, 64), INDEX | WAVE | TILE, WAVE | TILE),
     ((1, 300, 2048, 700), INDEX | QUERY | TILE, QUERY | TILE),
     ((4, 1, 2048, 512), QUERY | COMBINE, QUERY | COMBINE),
     ((1, 3, 2048, 64), WAVE, WAVE),

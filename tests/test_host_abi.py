@@ -114,7 +114,7 @@ def test_plan_indices_rejects_bad_args_without_device_work(libs):
     a.d = 256
     assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EUNSUPPORTED
     a = good_args()
-    a.flags = 32
+    a.flags = 64
     assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EINVAL
     a.flags = 8 | 16                           # both tile forms at once
     assert hip.sa_plan_indices(ctypes.byref(a), None) == SA_EINVAL
@@ -162,7 +162,7 @@ def test_library_exports_every_declared_symbol(libs):
     hip, _ = libs
     for name in declared_functions():
         assert hasattr(hip, name), f"{name} not exported"
-    assert hip.sa_abi_version() == 8
+    assert hip.sa_abi_version() == 9
     # the allocation-free entry point and its device array live in their own
     # library, so sa_forward's callers do not carry the array
     assert not hasattr(hip, "sa_forward_noalloc")
@@ -215,7 +215,7 @@ def test_forward_rejects_null_args(libs):
     ("q", 0, SA_EINVAL), ("o", 0, SA_EINVAL), ("sink", 0, SA_EINVAL),
     ("idx", 0, SA_EINVAL), ("kv", 0, SA_EINVAL),
     ("q", 0x10008, SA_EINVAL), ("o", 0x50002, SA_EINVAL), ("kv", 0x20004, SA_EINVAL),
-    ("scale", float("nan"), SA_EINVAL), ("flags", 32, SA_EINVAL), ("flags", 8 | 16, SA_EINVAL),
+    ("scale", float("nan"), SA_EINVAL), ("flags", 64, SA_EINVAL), ("flags", 8 | 16, SA_EINVAL),
     ("flags", 1 << 31, SA_EINVAL), ("workspace", 0x70008, SA_EINVAL),
 ])
 def test_forward_argument_errors(libs, field, value, code):
