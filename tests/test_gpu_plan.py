@@ -148,6 +148,17 @@ def test_capi_planned_launches(gpu_sa, shape, plain, planned):
     assert torch.equal(o, ref)
 
 
+def mixed_long(m, seed):
+    """topk 448 (above the one-wave kernel's): every third tile of windows
+    (shared), the others random rows of 8192 (per query), -1 slots."""
+    q, kv, sink, idx, sc = case(1, m, 8192, 448, seed=seed, minus1=0.05)
+    t = torch.arange(m, device=DEV)
+    win = ((torch.arange(448, device=DEV)[None] + 5 * t[:, None]) % 8192).to(torch.int32)
+    sel = (t // 8) % 3 == 0
+    idx[0, sel] = win[sel]
+    return q, kv, sink, idx, sc
+
+
 def placed_cases():
     """Shapes whose tiles number between half the CUs and the CUs: the plain
     call places them itself (no order kernel)."""
@@ -159,15 +170,20 @@ def placed_cases():
         "windows, ragged": lambda: windows(1, m - 5, 3000, seed=12),
         "per-query tiles": lambda: case(1, m // 2 + 8, 16384, 256, seed=13, minus1=0.1),
         "mixed, bad index": lambda: case(2, m // 2, 700, 128, seed=14, minus1=0.3),
+        "per-query tiles, long topk": lambda: case(1, m // 2 + 8, 16384, 512, seed=15,
+                                                   minus1=0.1),
+        "mixed, long topk": lambda: mixed_long(m - 11, seed=16),
     }
 
 
 @pytest.mark.parametrize("name", ["high locality", "windows, ragged", "per-query tiles",
-                                  "mixed, bad index"])
+                                  "mixed, bad index", "per-query tiles, long topk",
+                                  "mixed, long topk"])
 def test_placed_tiles_match_ordered(gpu_sa, name):
-    """A plain call that places its tiles itself equals the planned call,
-    whose tiles run in the tile order's placement, bit for bit (o, lse and
-    the error word). The plain call makes no tile order."""
+    """A plain call in the placed regime equals the planned call, whose tiles
+    run in the tile order's placement, bit for bit (o, lse and the error
+    word). The plain call makes no tile order; with topk up to 384 the short
+    queries run one wave each and the tile launch scans for shared tiles."""
     q, kv, sink, idx, sc = placed_cases()[name]()
     if name == "mixed, bad index":
         idx[1, 17, 3] = kv.shape[1] + 5
@@ -195,12 +211,15 @@ def test_placed_tiles_match_ordered(gpu_sa, name):
     expect_plan(q, kv, idx, tiles=True)
     ntiles = q.shape[0] * -(-q.shape[1] // 8)
     assert 2 * ntiles >= cus and ntiles <= cus, "the shape must be in the placed regime"
-    # topk <= 384: the per-query tiles run one wave per query, and a placed
-    # call has no order to make, so there is no QUERY launch
+    # topk <= 384: the per-query tiles run one wave per query; above, in the
+    # QUERY launch (a placed call has no order to make)
     pq = WAVE if idx.shape[2] <= 384 else QUERY
     assert k1 == INDEX | pq | TILE and k2 == pq | TILE
     assert torch.equal(o1, o2) and torch.equal(l1, l2)
     assert e1 == e2 == (1 if name == "mixed, bad index" else 0)
-    if name == "high locality":  # and the values themselves, on a sample
-        sampled_check(o1, q.cpu(), kv.cpu(), sink.cpu(), idx.cpu(), sc,
-                      [(0, 0), (1, 129), (2, 300), (3, 511)], "placed high locality")
+    samples = {"high locality": [(0, 0), (1, 129), (2, 300), (3, 511)],
+               "per-query tiles, long topk": [(0, 0), (0, q.shape[1] - 1)],
+               "mixed, long topk": [(0, 1), (0, 9), (0, q.shape[1] - 1)]}
+    if name in samples:  # and the values themselves, on a sample
+        sampled_check(o1, q.cpu(), kv.cpu(), sink.cpu(), idx.cpu(), sc, samples[name],
+                      f"placed {name}")
