@@ -123,6 +123,8 @@ def test_plan_indices_rejects_bad_args_without_device_work(libs):
     a = good_args()
     a.flags = 4                                # SA_FLAG_PLANNED is a valid bit
     assert host.sa_host_validate(ctypes.byref(a)) == SA_OK
+    a.flags = 32 | 8                           # SA_FLAG_TILE_ORDERED (version 9), with a form
+    assert host.sa_host_validate(ctypes.byref(a)) == SA_OK
 
 
 def test_ctypes_binding_matches_header_layout():
