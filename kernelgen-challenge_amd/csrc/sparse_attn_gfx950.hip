@@ -175,6 +175,9 @@ struct FwdParams {
   const int32_t* meta;
   int64_t tiles_per_b;
   OrderParams ord;
+  // sa_fwd_wave_kernel: walk each query's rows in ascending order (a batch's
+  // kv larger than an XCD's L2)
+  int sort_wave;
 };
 
 struct IndexParams {
@@ -707,6 +710,54 @@ __device__ __attribute__((noinline)) void sort_list(int32_t* s, int n) {
 #pragma unroll
   for (int r = 0; r < R; ++r) s[tid * R + r] = v[r];
   lds_barrier();
+}
+
+// Sorts s[0, n) ascending, as unsigned keys, with one wave (n <= 64 R): a
+// bitonic network over 64 R keys, R consecutive keys per lane, padded with
+// UINT32_MAX (never a row's byte offset, a multiple of the row size). Steps
+// whose partner key is in the same lane compare registers; the others
+// exchange keys by lane shuffles. Only s[0, n) is written back, so a list
+// that follows in LDS is untouched. Not inlined, for the reason sort_list is
+// not.
+template <int R>
+__device__ __attribute__((noinline)) void sort_list_wave(uint32_t* s, int n) {
+  constexpr int N = 64 * R;
+  const int lane = threadIdx.x & 63;
+  uint32_t v[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = lane * R + r;
+    v[r] = i < n ? s[i] : UINT32_MAX;
+  }
+#pragma unroll
+  for (int k = 2; k <= N; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < R) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if ((r & j) != 0) continue;
+          const uint32_t a = v[r], b = v[r | j];
+          const bool up = ((lane * R + r) & k) == 0;
+          v[r] = up ? min(a, b) : max(a, b);
+          v[r | j] = up ? max(a, b) : min(a, b);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const uint32_t o = uint32_t(__shfl_xor(int(v[r]), j / R));
+          const int i = lane * R + r;
+          const bool up = (i & k) == 0, low = (i & j) == 0;
+          v[r] = up == low ? min(v[r], o) : max(v[r], o);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = lane * R + r;
+    if (i < n) s[i] = v[r];
+  }
 }
 
 // One (query, topk part) unit of the per-query kernel. Leaves every wave past
@@ -1595,6 +1646,9 @@ constexpr int kWRows = 16;               // rows per step
 constexpr int kWPitch = kRowBytes + 48;  // LDS row pitch (bytes)
 constexpr int kWQueries = 2;             // queries per work-group
 constexpr int kWVAhead = 8;              // V fragments in flight in O += P . V
+// A batch's kv span (bytes) above which the wave kernel sorts each query's
+// rows: an XCD's L2 (4 MiB on MI355X)
+constexpr int64_t kWaveSortBytes = int64_t(4) << 20;
 // Slots per query the list holds. Against the 4-wave per-query kernel: topk
 // 128 1365 -> 1102 us/call at 64 x 1024 queries, topk 640 1232 -> 1260 at
 // 1 x 16384 (a longer list amortises that kernel's start), so the cap sits
@@ -1750,6 +1804,27 @@ __global__ void __launch_bounds__(64, 1) sa_fwd_wave_kernel(const FwdParams p) {
   // Q^T and the indices complete before the first gather is issued, so that
   // every later vmcnt(0) waits for the ring (and a Q^T issued after a gather)
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  if (p.sort_wave) {
+    // Each query walks its rows in ascending order: the queries resident on
+    // an XCD then sweep their batch's kv together, and a row that several of
+    // them name is fetched into the XCD's L2 once. The sorted sequence does
+    // not depend on the input order.
+    auto sort_query = [&](int j) {
+      uint32_t* s = reinterpret_cast<uint32_t*>(&sm.list[qsel(j)]);
+      const int n = qsel(j + 1) - qsel(j);
+      if (n <= 64)
+        sort_list_wave<1>(s, n);
+      else if (n <= 128)
+        sort_list_wave<2>(s, n);
+      else if (n <= 256)
+        sort_list_wave<4>(s, n);
+      else
+        sort_list_wave<8>(s, n);
+    };
+    static_assert(kWaveMaxTopk <= 64 * 8, "the sort covers a query's slots");
+    sort_query(0);
+    if (nq > 1) sort_query(1);
+  }
 
   // ---- the step stream ------------------------------------------------------------
   // The issue cursor (ji, si): query and step of the next step to gather. Lane
@@ -2931,6 +3006,9 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
   p.nsplit = plan.nsplit;
   p.split_len = plan.split_len;
   p.nblocks = plan.units * plan.nsplit;
+  // the wave kernel sorts its queries' rows when a batch's kv span exceeds an
+  // XCD's L2 (from the shape alone, so every path of a call sorts alike)
+  p.sort_wave = int64_t(a->kv_len) * a->skv[1] * 2 > kWaveSortBytes ? 1 : 0;
 
   // Short unsplit queries run one wave each (sa_fwd_wave_kernel): its list
   // holds 32-bit row offsets in a batch of kv. (Its epilogue's bf16 pair

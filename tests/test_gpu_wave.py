@@ -70,6 +70,11 @@ def per_query_queries(ws, b, m):
     (1, 261, 4096, 100, 0.2),    # ragged last tile (5 queries: a one-query work-group)
     (3, 89, 2048, 384, 0.1),     # the largest list; tiles of 8 + 1
     (1, 24, 600, 17, 0.0),       # one 16-row and one 1-row step (tiles shared here)
+    # a batch's kv above 4 MiB: each query's rows sorted ascending (2, 4 and
+    # 8 keys per lane)
+    (1, 300, 8192, 128, 0.1),
+    (1, 280, 6000, 256, 0.05),
+    (2, 133, 5000, 384, 0.1),
 ])
 def test_wave_tiles_full(gpu_sa, b, m, kv_len, topk, minus1):
     """Per-query tiles of a shared-row plan run one wave per query; every
@@ -153,3 +158,35 @@ def test_wave_topk_cap(gpu_sa):
         o, _, mask, err, _ = run(q, kv, sink, idx, sc, flags=PER_QUERY)
         assert err == 0 and mask == want
         check(o, sparse_attn_fp64(q, kv, sink, idx, sc), f"topk {topk}")
+
+def test_wave_sorted_rows_past_2gib(gpu_sa):
+    """A batch's kv of 2.3 GiB: the 32-bit row offsets of the wave kernel's
+    lists reach past 2^31, and each query's rows are sorted as unsigned
+    offsets. Half of every query's slots name rows beyond the 2^31-byte mark
+    (kv_len is above the shared-row limit: a per-query plan). Sampled queries
+    match the oracle on a compacted copy of the rows they name."""
+    kv_len = (1 << 21) + 300_000
+    b, m, topk = 1, 300, 128
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn(b, m, 16, 512, generator=g).to(torch.bfloat16)
+    sink = torch.randn(16, generator=g)
+    lo = torch.randint(0, 1 << 21, (b, m, topk // 2), generator=g, dtype=torch.int32)
+    hi = torch.randint(1 << 21, kv_len, (b, m, topk // 2), generator=g, dtype=torch.int32)
+    idx = torch.cat([hi, lo], dim=2)  # high offsets first: the sort must move them
+    idx[:, ::9, 5] = -1
+    gd = torch.Generator(device=DEV).manual_seed(78)
+    kv = torch.randn(b, kv_len, 512, generator=gd, device=DEV).to(torch.bfloat16)
+    p = expect_plan(q, kv, idx, 0, tiles=False)
+    if p["nsplit"] != 1:
+        pytest.skip(f"{m} queries split on this device")
+    o, _, mask, err, _ = run(q, kv, sink, idx, wl.SCALE)
+    assert err == 0 and mask == WAVE
+    sel = [0, 1, 9, 150, 299]
+    rows = torch.unique(idx[0, sel][idx[0, sel] >= 0])
+    remap = torch.full((kv_len,), -1, dtype=torch.int32)
+    remap[rows.long()] = torch.arange(rows.numel(), dtype=torch.int32)
+    idx_c = idx[:, sel].clone()
+    idx_c[idx_c >= 0] = remap[idx_c[idx_c >= 0].long()]
+    kv_c = kv[:, rows.to(DEV).long()].cpu()
+    exp = sparse_attn_fp64(q[:, sel], kv_c, sink, idx_c, wl.SCALE)
+    check(o.cpu()[:, sel], exp, "wave rows past 2^31")
