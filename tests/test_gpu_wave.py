@@ -190,3 +190,36 @@ def test_wave_sorted_rows_past_2gib(gpu_sa):
     kv_c = kv[:, rows.to(DEV).long()].cpu()
     exp = sparse_attn_fp64(q[:, sel], kv_c, sink, idx_c, wl.SCALE)
     check(o.cpu()[:, sel], exp, "wave rows past 2^31")
+
+@pytest.mark.parametrize("topk", [128, 400])
+def test_index_long_cache_many_tiles(gpu_sa, topk):
+    """kv_len 9 000 (the index kernel's 1 024-thread form, one work-group per
+    CU by its count table) with three tiles per CU: every third tile takes
+    windows (shared), the others random rows (per query). The modes come out
+    as built, per-query tiles equal the plain per-query plan bit for bit,
+    shared tiles agree within the tolerance, and samples match the oracle.
+    topk 128 runs the per-query tiles one wave each, 400 in the 4-wave
+    kernel."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    m = 8 * 3 * cus + 3
+    q, kv, sink, idx, sc = case(1, m, 9000, topk, seed=topk + 5, minus1=0.02)
+    t = torch.arange(m)
+    win = ((torch.arange(topk)[None] + 2 * t[:, None]) % 9000).to(torch.int32)
+    sel = (t // 8) % 3 == 0
+    idx[0, sel] = win[sel]
+    expect_plan(q, kv, idx, 0, tiles=True, nsplit=1)
+    o, _, mask, err, ws = run(q, kv, sink, idx, sc)
+    assert err == 0 and mask & INDEX and mask & TILE
+    pq = per_query_queries(ws, 1, m)[0]
+    # full tiles come out as built (the ragged last tile of 3 window queries
+    # is cheaper per query by the mode rule)
+    full = torch.arange(m) < m // 8 * 8
+    assert not pq[sel & full].any() and pq[~sel & full].all(), "modes as built"
+    o_p, _, _, _, _ = run(q, kv, sink, idx, sc, flags=PER_QUERY)
+    oc, opc = o.cpu(), o_p.cpu()
+    assert torch.equal(oc[0, pq], opc[0, pq])
+    d = (oc.float() - opc.float()).abs()
+    say(f"  long-cache index kernel, topk {topk}: shared vs per query max {d.max().item():.3e}")
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
+    s = [0, 9, 8 * 3 * 5, m // 2, m - 1]
+    check(oc[:, s], sparse_attn_fp64(q[:, s], kv, sink, idx[:, s], sc), f"long-cache index {topk}")
