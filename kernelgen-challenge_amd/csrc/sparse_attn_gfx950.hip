@@ -1090,13 +1090,24 @@ __device__ __forceinline__ void query_stream(const FwdParams& p, int64_t bi, int
 // vectors per thread, and twice the work-groups per CU): the contest shapes'
 // index kernel 64x1024-1024-128 36.7 -> 13.2 us, 16x4096-4096-128 40.0 ->
 // 21.3, 64x1024-1280-384 101 -> 73 (A/B, same box).
+// The one-wave kernel's list holds this many slots per query (queries with
+// topk up to it run one wave each). Against the 4-wave per-query kernel:
+// topk 128 1365 -> 1102 us/call at 64 x 1024 queries, topk 640 1232 -> 1260
+// at 1 x 16384 (a longer list amortises that kernel's start), so the cap sits
+// between them.
+constexpr int kWaveMaxTopk = 384;
 constexpr int kIdxThreadsNarrow = 512;
 constexpr int kIdxVecNarrow = 4;    // index vectors per thread per round
 constexpr int64_t kIdxWideKv = 8192;
 constexpr int kIdxSmallSlots = 4096;  // tile slots (8 topk) up to which 256 threads
 constexpr int kIdxScan = 4;   // LDS chunk reads per wave per batch
 
-template <int kIdxThreads, int kIdxVec>
+// kBits (long caches, topk <= kWaveMaxTopk, whose tiles usually go per
+// query): the tile's valid rows are first marked in a bitmap (the count
+// table's first kv_len / 8 bytes), which gives the union size and so the
+// mode; only a shared tile then clears the count table and counts, from the
+// same index registers (one round holds the tile's indices).
+template <int kIdxThreads, int kIdxVec, bool kBits>
 __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexParams p) {
   constexpr int kIdxWaves = kIdxThreads / 64;
   extern __shared__ unsigned long long s_count[];  // [kv_len], byte q = count in query q
@@ -1160,18 +1171,104 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
   int4 v0[kIdxVec];
   int q0v[kIdxVec];
   if (p.vec4) load4(0, v0, q0v);
+  // kBits without vec4: the tile's indices as int32, one round
+  int vs[4 * kIdxVec];
+  int qs[4 * kIdxVec];
+  if constexpr (kBits) {
+    static_assert(kIdxThreads * kIdxVec * 4 >= kTQ * kWaveMaxTopk, "one round holds a tile");
+    if (!p.vec4) {
+      const int nv = qt * topk;
+#pragma unroll
+      for (int u = 0; u < 4 * kIdxVec; ++u) {
+        const int e = u * kIdxThreads + tid;
+        const int qq = e / max(topk, 1);
+        qs[u] = qq;
+        vs[u] = e < nv ? ib[qq * p.si_m + (e - qq * topk)] : -1;
+      }
+    }
+    // ---- 0. mark: the union size and the mode ------------------------------------
+    uint32_t* s_bits = reinterpret_cast<uint32_t*>(s_count);
+    for (int i = tid; i < (kvl + 31) / 32; i += kIdxThreads) s_bits[i] = 0u;
+    if (tid == 0) {
+      s_nvalid = 0;
+      s_nunion = 0;
+    }
+    __syncthreads();
+    auto mark = [&](int v) {
+      const bool ok = v >= 0 && v < kvl;
+      if (ok) {
+        const uint32_t bit = 1u << (v & 31);
+        nfresh += (atomicOr(&s_bits[v >> 5], bit) & bit) == 0u ? 1 : 0;
+      }
+      bad = bad || (!ok && v != -1);
+      nvalid += __popcll(__ballot(ok));
+    };
+    if (p.vec4) {
+#pragma unroll
+      for (int u = 0; u < kIdxVec; ++u) {
+        mark(v0[u].x);
+        mark(v0[u].y);
+        mark(v0[u].z);
+        mark(v0[u].w);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4 * kIdxVec; ++u) mark(vs[u]);
+    }
+    if (bad && p.err != nullptr) flag_bad_index(p.err);
+    if (lane == 0 && nvalid != 0) atomicAdd(&s_nvalid, nvalid);
+    for (int off = 32; off > 0; off >>= 1) nfresh += __shfl_xor(nfresh, off);
+    if (lane == 0 && nfresh != 0) atomicAdd(&s_nunion, nfresh);
+    __syncthreads();
+    // the first setter of each row's bit counted it: s_nunion is the union size
+    const bool cheaper = shared_is_cheaper(s_nunion, s_nvalid, qt, p.placed_regime != 0);
+    if (p.force == 0 && !cheaper) {
+      if (tid == 0) {
+        int32_t* meta = p.meta + tile * kMetaInts;
+        meta[0] = s_nunion;
+        meta[1] = sa::kModePerQuery;
+        meta[2] = s_nvalid;
+        meta[3] = 0;
+      }
+      return;
+    }
+    __syncthreads();  // every thread has read the counts; the bitmap is free
+  }
   for (int i = tid; i < kvl; i += kIdxThreads) s_count[i] = 0ull;
   for (int i = tid; i < nchunks; i += kIdxThreads) s_cnz[i] = 0;
   if (tid == 0) {
     s_first = kvl;
-    s_nvalid = 0;
-    s_nunion = 0;
+    if (!kBits) {
+      s_nvalid = 0;
+      s_nunion = 0;
+    }
     s_bytes = 0;
   }
   __syncthreads();
 
   // ---- 1. count --------------------------------------------------------------
-  if (p.vec4) {
+  if constexpr (kBits) {
+    // the mode is decided and the valid slots counted: the counts alone
+    auto count_row = [&](int v, int qq) {
+      if (v >= 0 && v < kvl) {
+        atomicAdd(&s_count[v], 1ull << (8 * qq));
+        s_cnz[v >> 6] = 1;
+      }
+    };
+    if (p.vec4) {
+#pragma unroll
+      for (int u = 0; u < kIdxVec; ++u) {
+        count_row(v0[u].x, q0v[u]);
+        count_row(v0[u].y, q0v[u]);
+        count_row(v0[u].z, q0v[u]);
+        count_row(v0[u].w, q0v[u]);
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4 * kIdxVec; ++u) count_row(vs[u], qs[u]);
+    }
+    __syncthreads();
+  } else if (p.vec4) {
     count4(v0, q0v);
     for (int e0 = kIdxThreads * kIdxVec; e0 < nv4; e0 += kIdxThreads * kIdxVec) {
       int4 v[kIdxVec];
@@ -1195,25 +1292,27 @@ __global__ void __launch_bounds__(kIdxThreads) sa_tile_index_kernel(const IndexP
       for (int u = 0; u < 4 * kIdxVec; ++u) count(v[u], qv[u]);
     }
   }
-  if (bad && p.err != nullptr) flag_bad_index(p.err);
-  if (lane == 0 && nvalid != 0) atomicAdd(&s_nvalid, nvalid);
-  for (int off = 32; off > 0; off >>= 1) nfresh += __shfl_xor(nfresh, off);
-  if (lane == 0 && nfresh != 0) atomicAdd(&s_nunion, nfresh);
-  __syncthreads();
-  // Each row's first count found its word at 0 (LDS atomics on one word are
-  // serialised), so s_nunion is the union size, and the mode can be decided
-  // now: a per-query tile needs no union, so its scan and write are skipped.
-  // (A count carry can only make a tile per query, below.)
-  const bool cheaper = shared_is_cheaper(s_nunion, s_nvalid, qt, p.placed_regime != 0);
-  if (p.force == 0 && !cheaper) {
-    if (tid == 0) {
-      int32_t* meta = p.meta + tile * kMetaInts;
-      meta[0] = s_nunion;
-      meta[1] = sa::kModePerQuery;
-      meta[2] = s_nvalid;
-      meta[3] = 0;
+  if constexpr (!kBits) {
+    if (bad && p.err != nullptr) flag_bad_index(p.err);
+    if (lane == 0 && nvalid != 0) atomicAdd(&s_nvalid, nvalid);
+    for (int off = 32; off > 0; off >>= 1) nfresh += __shfl_xor(nfresh, off);
+    if (lane == 0 && nfresh != 0) atomicAdd(&s_nunion, nfresh);
+    __syncthreads();
+    // Each row's first count found its word at 0 (LDS atomics on one word
+    // are serialised), so s_nunion is the union size, and the mode can be
+    // decided now: a per-query tile needs no union, so its scan and write are
+    // skipped. (A count carry can only make a tile per query, below.)
+    const bool cheaper = shared_is_cheaper(s_nunion, s_nvalid, qt, p.placed_regime != 0);
+    if (p.force == 0 && !cheaper) {
+      if (tid == 0) {
+        int32_t* meta = p.meta + tile * kMetaInts;
+        meta[0] = s_nunion;
+        meta[1] = sa::kModePerQuery;
+        meta[2] = s_nvalid;
+        meta[3] = 0;
+      }
+      return;
     }
-    return;
   }
 
   // ---- 2. scan -----------------------------------------------------------------
@@ -1649,11 +1748,6 @@ constexpr int kWVAhead = 8;              // V fragments in flight in O += P . V
 // A batch's kv span (bytes) above which the wave kernel sorts each query's
 // rows: an XCD's L2 (4 MiB on MI355X)
 constexpr int64_t kWaveSortBytes = int64_t(4) << 20;
-// Slots per query the list holds. Against the 4-wave per-query kernel: topk
-// 128 1365 -> 1102 us/call at 64 x 1024 queries, topk 640 1232 -> 1260 at
-// 1 x 16384 (a longer list amortises that kernel's start), so the cap sits
-// between them.
-constexpr int kWaveMaxTopk = 384;
 constexpr int kWSlots = kWaveMaxTopk / 64;
 static_assert(kTQ % kWQueries == 0, "a tile's queries split evenly");
 static_assert(kWQueries == 2, "the cursor state is two queries' scalars");
@@ -3068,11 +3162,15 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
       const int64_t slots = kTQ * a->topk;
       const bool small1 = !wide && slots <= 256 * 4;
       const bool small4 = !wide && !small1 && slots <= kIdxSmallSlots;
+      // long caches with short queries: the mode from a bitmap first
+      const bool bits = wide && a->topk <= kWaveMaxTopk;
       const void* ik =
-          wide     ? reinterpret_cast<const void*>(sa_tile_index_kernel<1024, 2>)
-          : small1 ? reinterpret_cast<const void*>(sa_tile_index_kernel<256, 1>)
-          : small4 ? reinterpret_cast<const void*>(sa_tile_index_kernel<256, 4>)
-                   : reinterpret_cast<const void*>(sa_tile_index_kernel<kIdxThreadsNarrow, kIdxVecNarrow>);
+          bits     ? reinterpret_cast<const void*>(sa_tile_index_kernel<1024, 2, true>)
+          : wide   ? reinterpret_cast<const void*>(sa_tile_index_kernel<1024, 2, false>)
+          : small1 ? reinterpret_cast<const void*>(sa_tile_index_kernel<256, 1, false>)
+          : small4 ? reinterpret_cast<const void*>(sa_tile_index_kernel<256, 4, false>)
+                   : reinterpret_cast<const void*>(
+                         sa_tile_index_kernel<kIdxThreadsNarrow, kIdxVecNarrow, false>);
       if (lds > 65536 &&
           hipFuncSetAttribute(ik, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
         return SA_EHIP;

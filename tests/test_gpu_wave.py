@@ -223,3 +223,25 @@ def test_index_long_cache_many_tiles(gpu_sa, topk):
     assert d.max().item() <= 2e-2 and d.mean().item() <= 1e-3
     s = [0, 9, 8 * 3 * 5, m // 2, m - 1]
     check(oc[:, s], sparse_attn_fp64(q[:, s], kv, sink, idx[:, s], sc), f"long-cache index {topk}")
+
+def test_index_bitmap_mode_bad_index(gpu_sa):
+    """kv_len 12 000, topk 64: the index kernel decides each tile's mode from
+    a bitmap of its rows before it counts them. An out-of-range index in a
+    shared tile and one in a per-query tile set the error word; every other
+    slot counts, as in the oracle with those two slots masked."""
+    m = 8 * 40
+    q, kv, sink, idx, sc = case(1, m, 12000, 64, seed=91, minus1=0.05)
+    t = torch.arange(m)
+    win = ((torch.arange(64)[None] + t[:, None]) % 12000).to(torch.int32)
+    sel = (t // 8) % 2 == 0
+    idx[0, sel] = win[sel]
+    idx[0, 3, 10] = 12000            # a shared tile (tile 0)
+    idx[0, 9, 20] = -5               # a per-query tile (tile 1)
+    o, _, mask, err, ws = run(q, kv, sink, idx, sc)
+    assert err == 1 and mask & INDEX
+    pq = per_query_queries(ws, 1, m)[0]
+    assert not pq[:8].any() and pq[8:16].all()
+    ok = idx.clone()
+    ok[0, 3, 10] = -1
+    ok[0, 9, 20] = -1
+    check(o, sparse_attn_fp64(q, kv, sink, ok, sc), "bitmap mode, bad index")
