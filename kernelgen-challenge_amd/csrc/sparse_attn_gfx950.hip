@@ -19,19 +19,26 @@
 //   (one byte per query), writes the row union in ascending order (32-bit
 //   byte offsets) with an fp16 log2 multiplicity per (query, row), and marks
 //   the tile "shared" when the shared-row kernel would spend less CU time on
-//   it than the per-query kernel on its queries, else "per query".
+//   it than the per-query kernel on its queries, else "per query". With long
+//   caches and short queries the mode comes first, from a bitmap of the
+//   tile's rows, and only shared tiles are counted.
+// sa_order_kernel  one work-group: the tile order (a counting sort by
+//   descending step count, so the longest tiles are launched first) where no
+//   per-query launch makes it (index plans, and the ordered short-query
+//   launch).
 // sa_fwd_tile_kernel  one work-group per shared tile (128 query-head
 //   columns): gathers each union row once (LDS-DMA, 1 KiB per instruction),
 //   S^T = K . Q^T with each wave owning two queries, P through LDS, O += P . V
 //   with each wave owning a quarter of d; v_mfma_f32_32x32x16_bf16; the
 //   softmax of one 32-row half runs between the MFMAs of the next. A fixed
 //   per-column reference replaces rescaling; a tile whose scores jump above
-//   it runs its queries per query in place.
+//   it runs its queries per query in place. Work-group i runs entry i of the
+//   tile order, or (short-query plans) one work-group per CU walks the
+//   tiles' modes and runs the shared ones.
 // sa_fwd_query_kernel  one work-group (4 wave64s) per (query, topk part);
 //   in a shared-row plan (before the shared-row kernel) one per tile, which
 //   runs the queries of a per-query tile in turn, and work-group 0 makes the
-//   tile order: a counting sort by descending step count, so the longest
-//   tiles are launched first. Compacts the part's valid indices into LDS,
+//   tile order. Compacts the part's valid indices into LDS,
 //   then streams steps of 32 gathered rows through a ring of LDS buffers
 //   filled by LDS-DMA (4 buffers, or 2 and two work-groups per CU when the
 //   launch has at least two per CU). S^T = K . Q^T with v_mfma_f32_16x16x32_bf16 (wave w:
@@ -46,10 +53,13 @@
 //   group per two queries, a stream of 16-row steps through the wave's own
 //   2-deep LDS-DMA ring, no barrier. S^T = K . Q^T (16x16x32 MFMA, Q^T as
 //   an AGPR operand), the softmax inside the wave, O += P . V with
-//   v_mfma_f32_16x16x16_bf16 taking P from the S^T accumulators.
+//   v_mfma_f32_16x16x16_bf16 taking P from the S^T accumulators. Each
+//   query's rows are sorted ascending when a batch's kv exceeds an XCD's L2.
 // sa_combine_kernel  merges the topk parts of one (query, head), folds the
 //   sink and stores bf16.
 // sa_merge_kernel  merges caller-supplied (o, lse) partials (sa_merge).
+// sa_pad_heads_kernel, sa_unpad_heads_kernel  calls with 1, 2, 4 or 8 heads
+//   run on a 16-head copy in the workspace (q zero-padded in, o copied out).
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -3181,8 +3191,9 @@ int forward16(const sa_args* a, hipStream_t stream, void* const* events, uint32_
     }
     // The per-query launch: one work-group per tile runs the queries of a
     // per-query tile (the others return at once), and work-group 0 makes the
-    // tile order when this call makes one (an index plan and a short-query
-    // plan make it in sa_order_kernel instead, below).
+    // tile order when this call makes one (an index plan makes it in
+    // sa_order_kernel instead, below; a short-query plan makes none, unless a
+    // flag asks for the ordered tile launch).
     // (Running a placed call's per-query tiles in the tile kernel instead,
     // through the branch that reruns aborted tiles, makes the compiler spill
     // the kernel's 256 AGPR accumulators.)
