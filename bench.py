@@ -86,6 +86,10 @@ PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 EAGER = True
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 H, D = wl.NUM_HEADS, wl.HEAD_DIM
+# A call of one kernel is that kernel's dispatch plus a launch; timed in
+# separate loops the two can cross by their run-to-run spread. Beyond this
+# fraction a kernel time above the call's voids the roofline fraction.
+KERNEL_OVER_CALL_TOL = 0.01
 KERNEL_NAMES = {"index": "sa_tile_index_kernel", "order": "sa_order_kernel",
                 "tile": "sa_fwd_tile_kernel", "query": "sa_fwd_query_kernel",
                 "combine": "sa_combine_kernel", "wave": "sa_fwd_wave_kernel"}
@@ -332,10 +336,17 @@ def roofline(name, flops, compulsory, times, shares, us_per_call):
     roof["kernel"] = KERNEL_NAMES[dom]
     roof["kernel_us"] = round(times[dom] * 1e3, 2)
     roof["kernel_timing"] = "HIP events taking the dispatch timestamps (hipExtLaunchKernel)"
-    if times[dom] * 1e3 > us_per_call:
+    over = times[dom] * 1e3 / us_per_call
+    if over > 1.0 + KERNEL_OVER_CALL_TOL:
         # a kernel cannot outlast the call that launched it: the measurement is wrong
         roof["frac"] = None
         roof["frac_note"] = f"kernel_us {roof['kernel_us']} exceeds us_per_call {us_per_call}"
+    elif over > 1.0:
+        # a call of one kernel: the two, timed in separate loops, agree within
+        # their spread
+        roof["frac_note"] = (f"kernel_us {roof['kernel_us']} is {100 * (over - 1):.2f} % above "
+                             f"us_per_call {us_per_call} (separate loops; within "
+                             f"{100 * KERNEL_OVER_CALL_TOL:.0f} %)")
     roof["work_share"] = round(share, 4)
     roof["kernel_us_all"] = {KERNEL_NAMES[k]: round(v * 1e3, 2) for k, v in times.items()}
     roof["sources"] = digest

@@ -93,7 +93,9 @@ def test_source_digest_covers_kernel_sources(tmp_path, monkeypatch):
 def test_roofline_record_checks_provenance(monkeypatch):
     """frac comes from the live kernel time; the committed profile is quoted
     beside it with its own frac; a traffic figure from other sources is
-    dropped with the reason; a kernel time above the call time voids frac."""
+    dropped with the reason; a kernel time more than 1 % above the call
+    time voids frac (less is the spread of two loops timing a one-kernel
+    call, noted beside it)."""
     flops = 4.0 * 16 * 512 * 1000
     monkeypatch.setattr(bench, "traffic_of", lambda name: {
         "bytes_per_launch": 123, "sources": "0" * 16, "profile": "p.txt"})
@@ -109,6 +111,9 @@ def test_roofline_record_checks_provenance(monkeypatch):
     assert abs(r["profile"]["live_over_profile"] - 1.0) < 1e-9
     r = bench.roofline("causal_prefill", flops, 1.0, {"tile": 0.2}, {"tile": 1.0}, 150.0)
     assert r["frac"] is None and "exceeds" in r["frac_note"]
+    # a one-kernel call whose kernel reads 0.5 % above it (separate loops)
+    r = bench.roofline("causal_prefill", flops, 1.0, {"tile": 0.1005}, {"tile": 1.0}, 100.0)
+    assert r["frac"] is not None and "above" in r["frac_note"]
 
 
 def test_gemm_ceiling_shapes_follow_the_moe_workload():
