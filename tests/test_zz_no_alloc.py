@@ -3,8 +3,9 @@
 equal sa_forward's (with a caller workspace)
 bit for bit, since both run the same kernels, on two calls in a row where the
 second input is smaller (the library's scratch array then holds the first
-call's contents). Each plan kind is covered: shared-row tiles, split-topk and
-per query. A call that needs more scratch than the array holds is refused
+call's contents). Each plan kind is covered: shared-row tiles, split-topk,
+per query, and short queries over a long cache. A call that needs more
+scratch than the array holds is refused
 with SA_ESCRATCH before any device work.
 """
 import ctypes
@@ -60,6 +61,9 @@ CASES = {
     "tiles": ((1, 512, 2048, 1024, 1, 0.1), (1, 64, 700, 256, 2, 0.0)),
     "split": ((8, 1, 32768, 2048, 3, 0.0), (4, 1, 9000, 1000, 4, 0.05)),
     "per query": ((1, 300, 20000, 128, 5, 0.2), (1, 40, 3000, 64, 6, 0.0)),
+    # short queries over a long cache: the index kernel's bitmap-first mode,
+    # the scanning tile launch and sorted rows in the wave kernel
+    "short queries, long cache": ((1, 300, 9000, 128, 10, 0.05), (1, 80, 8192, 64, 11, 0.0)),
 }
 
 
